@@ -1,0 +1,349 @@
+"""CPU oracle for the int8-nk quantized-linear path (TEST INFRASTRUCTURE ONLY).
+
+Two numpy-facing bindings live here:
+
+* ``Oracle``   — our C restatement (``oracle/ovoracle.c`` -> ``liboracle.so``),
+  the parity checker for the HIP kernels and the "port" CPU baseline;
+* ``Reference`` — the reference's own CPU kernels compiled from
+  ``/root/reference/cpp/src/backend/cpu/{gemm,ops_cpu,conv_cpu}.cpp`` plus our
+  extern "C" shim (``oracle/_ref/libovref.so``), used to pin the restatement and
+  as the "reference" CPU baseline where its AVX-VNNI dispatch is available.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
+import this package.  The product (``ovnative_amd``) never does.
+
+Byte formats follow the reference: activations are quantised per 32-k block to
+``u8 = q + 128`` (K tail padded with byte 0) with one fp32 scale per block
+(``cpp/src/backend/cpu/gemm.cpp:379-430``); weights are int8 ``[N, K]`` with one
+fp32 scale per output row (``tools/convert_weights.py:130-135``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libovref.so")
+REF_TREE = "/root/reference/cpp"
+
+_i64 = C.c_int64
+_f32 = C.c_float
+_p = C.c_void_p
+
+
+def build(ref: bool = True) -> None:
+    """Compile liboracle.so (and oracle/_ref when the reference tree is mounted)."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE, "all"], check=True)
+    if ref and os.path.isdir(REF_TREE):
+        subprocess.run(["make", "-s", "-B", "-C", HERE, "ref"], check=True)
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def kb_of(K: int) -> int:
+    return (K + 31) // 32
+
+
+class Oracle:
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            build(ref=False)
+        self.lib = L = C.CDLL(path)
+        sig = {
+            "ovo_quant_bytes": (_i64, [_i64, _i64]),
+            "ovo_quant_scales": (_i64, [_i64, _i64]),
+            "ovo_quantize_weight_rows": (None, [_i64, _i64, _p, _p, _p]),
+            "ovo_quantize_u8": (None, [_i64, _i64, _p, _p, _p]),
+            "ovo_rmsnorm_f32": (None, [_p, _p, _p, _i64, _i64, _f32]),
+            "ovo_rmsnorm_quantize_u8": (None, [_i64, _i64, _p, _p, _f32, _p, _p]),
+            "ovo_exp256": (_f32, [_f32]),
+            "ovo_silu_mul_f32": (None, [_p, _p, _p, _i64]),
+            "ovo_silu_mul_quantize_u8": (None, [_i64, _i64, _p, _p, _p, _p]),
+            "ovo_block_dots": (None, [_i64, _i64, _i64, _p, _p, _p]),
+            "ovo_linear_q": (None, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, C.c_int]),
+            "ovo_packed_bytes": (_i64, [_i64, _i64]),
+            "ovo_wsum_elems": (_i64, [_i64, _i64]),
+            "ovo_pack": (None, [_i64, _i64, _p, _p, _p]),
+            "ovo_fast_available": (C.c_int, []),
+            "ovo_linear_q_packed": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64,
+                                              C.c_int]),
+            "ovo_num_threads": (C.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # -- weights -----------------------------------------------------------
+    def quantize_weight_rows(self, W: np.ndarray):
+        W = np.ascontiguousarray(W, dtype=np.float32)
+        N, K = W.shape
+        q = np.empty((N, K), np.int8)
+        s = np.empty(N, np.float32)
+        self.lib.ovo_quantize_weight_rows(N, K, _ptr(W), _ptr(q), _ptr(s))
+        return q, s
+
+    # -- activation quantizers (reference u8 format) ------------------------
+    def quantize(self, A: np.ndarray):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        M, K = A.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        self.lib.ovo_quantize_u8(M, K, _ptr(A), _ptr(aq), _ptr(asc))
+        return aq, asc
+
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray, eps: float = 1e-6):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        self.lib.ovo_rmsnorm_f32(_ptr(out), _ptr(x), _ptr(w), x.shape[0], x.shape[1], eps)
+        return out
+
+    def rmsnorm_quantize(self, x: np.ndarray, w: np.ndarray, eps: float = 1e-6):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        M, K = x.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        self.lib.ovo_rmsnorm_quantize_u8(M, K, _ptr(x), _ptr(w), eps, _ptr(aq), _ptr(asc))
+        return aq, asc
+
+    def exp256(self, x: float) -> float:
+        return float(self.lib.ovo_exp256(x))
+
+    def silu_mul(self, g: np.ndarray, u: np.ndarray):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.ovo_silu_mul_f32(_ptr(out), _ptr(g), _ptr(u), g.size)
+        return out
+
+    def silu_mul_quantize(self, g: np.ndarray, u: np.ndarray):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        M, K = g.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        self.lib.ovo_silu_mul_quantize_u8(M, K, _ptr(g), _ptr(u), _ptr(aq), _ptr(asc))
+        return aq, asc
+
+    # -- GEMM ----------------------------------------------------------------
+    def block_dots(self, aq: np.ndarray, W: np.ndarray) -> np.ndarray:
+        """int32 [M, N, Kb]: Σ_{k in block} (aq-128)·W[n,k]."""
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        M = aq.shape[0]
+        out = np.empty((M, N, kb_of(K)), np.int32)
+        self.lib.ovo_block_dots(M, N, K, _ptr(aq), _ptr(W), _ptr(out))
+        return out
+
+    def linear_q(self, aq, asc, W, wscale, C=None, accumulate=False) -> np.ndarray:
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        M = aq.shape[0]
+        if C is None:
+            C = np.zeros((M, N), np.float32)
+        else:
+            C = np.array(C, dtype=np.float32, copy=True, order="C")
+        wscale = np.ascontiguousarray(wscale, dtype=np.float32)
+        self.lib.ovo_linear_q(M, N, K, _ptr(aq), _ptr(asc), _ptr(W), _ptr(wscale), _ptr(C),
+                              C.shape[1], int(bool(accumulate)))
+        return C
+
+    def linear(self, A, W, wscale, C=None, accumulate=False):
+        """Quantise fp32 activations, then linear_q (gemm.cpp:829-845 / :864-882)."""
+        aq, asc = self.quantize(A)
+        return self.linear_q(aq, asc, W, wscale, C, accumulate)
+
+    # -- packed AVX-512 form (timing) ---------------------------------------
+    def fast_available(self) -> bool:
+        return bool(self.lib.ovo_fast_available())
+
+    def pack(self, W: np.ndarray):
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        packed = np.empty(self.lib.ovo_packed_bytes(N, K), np.int8)
+        wsum = np.empty(self.lib.ovo_wsum_elems(N, K), np.int32)
+        self.lib.ovo_pack(N, K, _ptr(W), _ptr(packed), _ptr(wsum))
+        return packed, wsum
+
+    def linear_q_packed(self, aq, asc, packed, wsum, N, K, wscale, C, accumulate=False):
+        rc = self.lib.ovo_linear_q_packed(aq.shape[0], N, K, _ptr(aq), _ptr(asc), _ptr(packed),
+                                          _ptr(wsum), _ptr(wscale), _ptr(C), C.shape[1],
+                                          int(bool(accumulate)))
+        if rc != 0:
+            raise RuntimeError("AVX-512 VNNI not available on this host")
+        return C
+
+    def num_threads(self) -> int:
+        return int(self.lib.ovo_num_threads())
+
+
+class Reference:
+    """The reference's compiled CPU kernels (see ``oracle/ref_shim.cpp``)."""
+
+    def __init__(self, path: str = REF_LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = L = C.CDLL(path)
+        sig = {
+            "ovref_vnni_available": (C.c_int, []),
+            "ovref_kernel_name": (C.c_char_p, []),
+            "ovref_enable_ftz": (None, []),
+            "ovref_s8_nk_quantize": (C.c_int, [_i64, _i64, _p, _p, _p]),
+            "ovref_rmsnorm_quantize": (C.c_int, [_i64, _i64, _p, _p, _f32, _p, _p]),
+            "ovref_silu_mul_quantize": (C.c_int, [_i64, _i64, _p, _p, _p, _p]),
+            "ovref_rmsnorm_into": (None, [_p, _p, _p, _i64, _i64, _f32]),
+            "ovref_silu_mul": (None, [_p, _p, _p, _i64]),
+            "ovref_packed_bytes": (_i64, [_i64, _i64]),
+            "ovref_wsum_elems": (_i64, [_i64, _i64]),
+            "ovref_pack": (None, [_i64, _i64, _p, _p, _p]),
+            "ovref_linear_packed_q": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
+                                                C.c_int]),
+            "ovref_linear_packed": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, C.c_int]),
+            "ovref_linear_packed_q_sliced": (C.c_int, [_i64, _i64, _p, _p, _p, _p, _p, _p, _p,
+                                                       C.c_int]),
+            "ovref_qk_norm_rope": (None, [_p, _p, _p, _p, _i64, C.c_int, C.c_int, C.c_int, _p,
+                                          _f32, _f32]),
+            "ovref_attention_head": (None, [_p, _i64, _p, _p, _i64, _p, C.c_int, C.c_int, _f32,
+                                            _p, _i64]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    def vnni_available(self) -> bool:
+        return bool(self.lib.ovref_vnni_available())
+
+    def kernel_name(self) -> str:
+        return self.lib.ovref_kernel_name().decode()
+
+    def quantize(self, A):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        M, K = A.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        if self.lib.ovref_s8_nk_quantize(M, K, _ptr(A), _ptr(aq), _ptr(asc)) != 0:
+            raise RuntimeError("reference s8_nk_quantize failed")
+        return aq, asc
+
+    def rmsnorm_quantize(self, x, w, eps=1e-6):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        M, K = x.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        if self.lib.ovref_rmsnorm_quantize(M, K, _ptr(x), _ptr(w), eps, _ptr(aq), _ptr(asc)):
+            raise RuntimeError("reference rmsnorm_quantize failed")
+        return aq, asc
+
+    def silu_mul_quantize(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        M, K = g.shape
+        aq = np.empty((M, kb_of(K) * 32), np.uint8)
+        asc = np.empty((M, kb_of(K)), np.float32)
+        if self.lib.ovref_silu_mul_quantize(M, K, _ptr(g), _ptr(u), _ptr(aq), _ptr(asc)):
+            raise RuntimeError("reference silu_mul_quantize failed")
+        return aq, asc
+
+    def rmsnorm(self, x, w, eps=1e-6):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        out = np.empty_like(x)
+        self.lib.ovref_rmsnorm_into(_ptr(out), _ptr(x), _ptr(w), x.shape[0], x.shape[1], eps)
+        return out
+
+    def silu_mul(self, g, u):
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        u = np.ascontiguousarray(u, dtype=np.float32)
+        out = np.empty_like(g)
+        self.lib.ovref_silu_mul(_ptr(out), _ptr(g), _ptr(u), g.size)
+        return out
+
+    def pack(self, W):
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        packed = np.empty(self.lib.ovref_packed_bytes(N, K), np.int8)
+        wsum = np.empty(self.lib.ovref_wsum_elems(N, K), np.int32)
+        self.lib.ovref_pack(N, K, _ptr(W), _ptr(packed), _ptr(wsum))
+        return packed, wsum
+
+    def linear_q_packed(self, aq, asc, packed, wsum, N, K, wscale, C, accumulate=False):
+        wscale = np.ascontiguousarray(wscale, dtype=np.float32)
+        if self.lib.ovref_linear_packed_q(aq.shape[0], N, K, _ptr(aq), _ptr(asc), _ptr(packed),
+                                          _ptr(wsum), _ptr(wscale), _ptr(C),
+                                          int(bool(accumulate))):
+            raise RuntimeError("reference linear_s8_nk_packed_q failed")
+        return C
+
+    def linear_q(self, aq, asc, W, wscale, C=None, accumulate=False):
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        packed, wsum = self.pack(W)
+        if C is None:
+            C = np.zeros((aq.shape[0], N), np.float32)
+        else:
+            C = np.array(C, dtype=np.float32, copy=True, order="C")
+        return self.linear_q_packed(aq, asc, packed, wsum, N, K, wscale, C, accumulate)
+
+    def linear(self, A, W, wscale, C=None, accumulate=False):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        packed, wsum = self.pack(W)
+        C = np.zeros((A.shape[0], N), np.float32) if C is None else np.array(C, np.float32)
+        wscale = np.ascontiguousarray(wscale, dtype=np.float32)
+        if self.lib.ovref_linear_packed(A.shape[0], N, K, _ptr(A), _ptr(packed), _ptr(wsum),
+                                        _ptr(wscale), _ptr(C), int(bool(accumulate))):
+            raise RuntimeError("reference linear_s8_nk_packed failed")
+        return C
+
+    def block_dots(self, aq, W):
+        """Per-block int32 through the reference's public API: with asc one-hot on
+        block b and wscale = 1, the epilogue returns fma(float(acc_b), 1, 0) =
+        float(acc_b), exact because |acc_b| < 2^24."""
+        W = np.ascontiguousarray(W, dtype=np.int8)
+        N, K = W.shape
+        M, Kb = aq.shape[0], kb_of(K)
+        packed, wsum = self.pack(W)
+        ones = np.ones(N, np.float32)
+        out = np.empty((M, N, Kb), np.int32)
+        for b in range(Kb):
+            asc = np.zeros((M, Kb), np.float32)
+            asc[:, b] = 1.0
+            C = np.zeros((M, N), np.float32)
+            self.linear_q_packed(aq, asc, packed, wsum, N, K, ones, C)
+            out[:, :, b] = C.astype(np.int32)
+        return out
+
+    def linear_q_sliced(self, aq, asc, W_slices, scale_slices):
+        """Merged [sum N, K] matrix with one C per slice (gemm.cpp:776-827)."""
+        K = W_slices[0].shape[1]
+        Wc = np.ascontiguousarray(np.concatenate(W_slices, axis=0), dtype=np.int8)
+        sc = np.ascontiguousarray(np.concatenate(scale_slices), dtype=np.float32)
+        packed, wsum = self.pack(Wc)
+        Ns = np.array([w.shape[0] for w in W_slices], np.int64)
+        outs = [np.zeros((aq.shape[0], int(n)), np.float32) for n in Ns]
+        ptrs = (C.c_void_p * len(outs))(*[o.ctypes.data for o in outs])
+        rc = self.lib.ovref_linear_packed_q_sliced(aq.shape[0], K, _ptr(aq), _ptr(asc),
+                                                   _ptr(packed), _ptr(wsum), _ptr(sc),
+                                                   _ptr(Ns), C.cast(ptrs, C.c_void_p),
+                                                   len(outs))
+        if rc == -2:
+            raise ValueError("sliced GEMM: each slice N must be a positive multiple of 64")
+        if rc != 0:
+            raise RuntimeError("reference sliced GEMM failed")
+        return outs
+
+
+def reference_available() -> bool:
+    return os.path.exists(REF_LIB_PATH)

@@ -1,0 +1,438 @@
+/*
+ * ovoracle.c — CPU restatement of OVNative's int8-nk quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker and the CPU
+ * baseline for the HIP implementation in ovnative_amd/.  Nothing in the
+ * product links, loads or calls it; only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg do.
+ *
+ * Every function restates one piece of the reference's arithmetic, in the
+ * reference's operation order, so that its outputs are the reference's bits.
+ * References are relative to the AFun9/ovnative tree:
+ *
+ *   ovo_quantize_weight_rows   tools/convert_weights.py:130-135  (quantize_int8)
+ *   ovo_quantize_u8            cpp/src/backend/cpu/gemm.cpp:379-430 (quantize_a_u8),
+ *                              entry point :709-720 (s8_nk_quantize)
+ *   ovo_rmsnorm_f32            cpp/src/backend/cpu/ops_cpu.cpp:38-62 (rmsnorm_avx2)
+ *   ovo_rmsnorm_quantize_u8    cpp/src/backend/cpu/gemm.cpp:638-707 (rmsnorm_quantize_avx2)
+ *   ovo_exp256                 cpp/src/backend/cpu/ops_cpu.cpp:75-92 (exp256_ps, one lane)
+ *   ovo_silu_mul_f32           cpp/src/backend/cpu/ops_cpu.cpp:126-136 (silu_mul_avx2)
+ *   ovo_silu_mul_quantize_u8   cpp/src/backend/cpu/ops_cpu.cpp:144-198 (silu_mul_quant_avx2)
+ *   ovo_block_dots             cpp/src/backend/cpu/gemm.cpp:455-474 (acc - 128*wsum per block)
+ *   ovo_linear_q               cpp/src/backend/cpu/gemm.cpp:432-504 (vnni_tile_at epilogue)
+ *   ovo_pack / ovo_linear_q_packed   the same arithmetic on AVX-512 VNNI, for timing
+ *
+ * "The reference's arithmetic" means the reference as its own build compiles it:
+ * g++ -O3 -std=c++17.  For C++, GCC's default is -ffp-contract=fast, so some
+ * mul/add pairs written separately in the source are single fused operations in
+ * the reference binary (exp256's range reduction, "1 + exp" in silu, the
+ * RMSNorm scalar tail).  Those places are called out below.
+ *
+ * Numerics that the restatement must keep (and that the HIP kernels keep):
+ *   - activation blocks are 32 k wide; scale = amax/127.0f, inv = 127.0f/amax
+ *     (0 when amax == 0), q = clamp(RNE(a*inv), -127, 127); a product that
+ *     cvtps_epi32 cannot represent (NaN, |x| >= 2^31) becomes INT_MIN and
+ *     therefore clamps to -127;
+ *   - the reference stores q + 128 as u8 and pads the K tail with byte 0;
+ *   - per output: f = fma((float)acc_b, asc[m,b], f) for b = 0..Kb-1, then
+ *     o = f * wscale[n]; the residual variant then rounds o + C separately.
+ *
+ * Build: oracle/Makefile (gcc, ISO C, -ffp-contract=off so that no mul+add
+ * pair is fused behind our back: the reference is built with -std=c++17,
+ * under which GCC does not contract either).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+#define OVO_API __attribute__((visibility("default")))
+
+static inline int64_t kb_of(int64_t K) { return (K + 31) / 32; }
+
+/* cvtps_epi32 semantics in round-to-nearest-even mode. */
+static inline int32_t cvt_rne_i32(float x) {
+  if (!(fabsf(x) < 2147483648.0f)) return INT32_MIN;
+  return (int32_t)nearbyintf(x);
+}
+
+static inline uint8_t quant_u8(float v, float inv) {
+  int32_t z = cvt_rne_i32(v * inv);
+  z = z < -127 ? -127 : (z > 127 ? 127 : z);
+  return (uint8_t)(z + 128);
+}
+
+/* Quantise `kn` (<= 32) values of one block into q[0..31]; returns the block scale. */
+static float quant_block_u8(const float* v, int64_t kn, uint8_t* q) {
+  float amax = 0.f;
+  for (int64_t i = 0; i < kn; ++i) {
+    const float a = fabsf(v[i]);
+    amax = a > amax ? a : amax;
+  }
+  const float scale = amax / 127.0f;
+  const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+  for (int64_t i = 0; i < kn; ++i) q[i] = quant_u8(v[i], inv);
+  for (int64_t i = kn; i < 32; ++i) q[i] = 0;
+  return scale;
+}
+
+OVO_API int64_t ovo_quant_bytes(int64_t M, int64_t K) { return M * kb_of(K) * 32; }
+OVO_API int64_t ovo_quant_scales(int64_t M, int64_t K) { return M * kb_of(K); }
+
+/* tools/convert_weights.py:130-135: per output row, scale = max(absmax/127, 1e-12)
+ * in float32; q = clip(rint(w/scale), -127, 127). */
+OVO_API void ovo_quantize_weight_rows(int64_t N, int64_t K, const float* W, int8_t* q,
+                                      float* scale) {
+  const float floor_scale = 1e-12f;
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const float* row = W + n * K;
+    float amax = 0.f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float a = fabsf(row[k]);
+      amax = a > amax ? a : amax;
+    }
+    float s = amax / 127.0f;
+    s = s > floor_scale ? s : floor_scale;
+    scale[n] = s;
+    for (int64_t k = 0; k < K; ++k) {
+      float r = rintf(row[k] / s);
+      r = r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
+      q[n * K + k] = (int8_t)r;
+    }
+  }
+}
+
+/* cpp/src/backend/cpu/gemm.cpp:379-430 */
+OVO_API void ovo_quantize_u8(int64_t M, int64_t K, const float* A, uint8_t* aq, float* asc) {
+  if (M <= 0 || K <= 0) return;
+  const int64_t Kb = kb_of(K), Kp = Kb * 32;
+#pragma omp parallel for schedule(static) if (M >= 32)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t b = 0; b < Kb; ++b) {
+      const int64_t k0 = b * 32, kn = (K - k0 < 32) ? (K - k0) : 32;
+      asc[m * Kb + b] = quant_block_u8(A + m * K + k0, kn, aq + m * Kp + k0);
+    }
+  }
+}
+
+/* Row scale of cpp/src/backend/cpu/ops_cpu.cpp:38-62: eight fma partial sums
+ * (element i feeds partial i%8, in increasing i), summed left to right, then
+ * the scalar tail (cols % 8) added one square at a time. */
+static float rms_scale(const float* row, int64_t cols, float eps) {
+  float lanes[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t i = 0;
+  for (; i + 8 <= cols; i += 8)
+    for (int j = 0; j < 8; ++j) lanes[j] = fmaf(row[i + j], row[i + j], lanes[j]);
+  float sum = lanes[0];
+  for (int j = 1; j < 8; ++j) sum = sum + lanes[j];
+  /* The scalar tail loop (`sum += row[i]*row[i]`, at most 7 iterations) is what
+   * GCC 11 vectorises: with 4 or more elements left, the first 4 squares are
+   * rounded (vmulps xmm) and added in order; every remaining element is one
+   * fused vfmadd231ss. */
+  const int64_t t = cols - i;
+  int64_t j = 0;
+  if (t >= 4)
+    for (; j < 4; ++j) {
+      const float sq = row[i + j] * row[i + j];
+      sum = sum + sq;
+    }
+  for (; j < t; ++j) sum = fmaf(row[i + j], row[i + j], sum);
+  return 1.f / sqrtf(sum / (float)cols + eps);
+}
+
+OVO_API void ovo_rmsnorm_f32(float* dst, const float* src, const float* w, int64_t rows,
+                             int64_t cols, float eps) {
+#pragma omp parallel for schedule(static) if (rows >= 32)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* row = src + r * cols;
+    const float s = rms_scale(row, cols, eps);
+    for (int64_t i = 0; i < cols; ++i) dst[r * cols + i] = (row[i] * s) * w[i];
+  }
+}
+
+/* cpp/src/backend/cpu/gemm.cpp:638-707 — byte-identical to rmsnorm then quantise. */
+OVO_API void ovo_rmsnorm_quantize_u8(int64_t rows, int64_t cols, const float* x, const float* w,
+                                     float eps, uint8_t* aq, float* asc) {
+  if (rows <= 0 || cols <= 0) return;
+  const int64_t Kb = kb_of(cols), Kp = Kb * 32;
+#pragma omp parallel for schedule(static) if (rows >= 32)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* row = x + r * cols;
+    const float s = rms_scale(row, cols, eps);
+    float v[32];
+    for (int64_t b = 0; b < Kb; ++b) {
+      const int64_t k0 = b * 32, kn = (cols - k0 < 32) ? (cols - k0) : 32;
+      for (int64_t i = 0; i < kn; ++i) v[i] = (row[k0 + i] * s) * w[k0 + i];
+      asc[r * Kb + b] = quant_block_u8(v, kn, aq + r * Kp + k0);
+    }
+  }
+}
+
+/* One lane of exp256_ps, cpp/src/backend/cpu/ops_cpu.cpp:75-92, as GCC 11 compiles
+ * it for the reference (-O3 -std=c++17; for C++ GCC's default is
+ * -ffp-contract=fast): clamp to [-87, 88], n = RNE(x*log2e), r = x - n*ln2 as ONE
+ * fused op (vfnmadd), degree-6 Horner with fma, then 2^n built in the exponent
+ * field.  Returns the polynomial p and the power sc separately because the
+ * caller decides how p*sc is rounded: alone it is a plain multiply (softmax),
+ * under "1 + exp(..)" GCC fuses it into fma(p, sc, 1) (silu). */
+static inline void exp256_parts(float x, float* p_out, float* sc_out) {
+  x = x < 88.0f ? x : 88.0f; /* minps returns the second operand on NaN */
+  x = x > -87.0f ? x : -87.0f;
+  const float n = nearbyintf(x * 1.4426950408889634f);
+  const float r = fmaf(-n, 0.6931471805599453f, x);
+  float p = 1.0f / 720;
+  p = fmaf(p, r, 1.0f / 120);
+  p = fmaf(p, r, 1.0f / 24);
+  p = fmaf(p, r, 1.0f / 6);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int32_t ni = cvt_rne_i32(n);
+  const uint32_t bits = (uint32_t)(ni + 127) << 23;
+  memcpy(sc_out, &bits, 4);
+  *p_out = p;
+}
+
+OVO_API float ovo_exp256(float x) {
+  float p, sc;
+  exp256_parts(x, &p, &sc);
+  return p * sc;
+}
+
+/* silu(g)*u on an 8-wide SIMD lane (ops_cpu.cpp:126-142): d = 1 + exp(0 - g)
+ * compiles to fma(p, sc, 1); then (g / d) * u.  The scalar tail (ops_cpu.cpp:23)
+ * calls libm expf and rounds every step. */
+static inline float silu_up_lane(float g, float u) {
+  float p, sc;
+  exp256_parts(0.0f - g, &p, &sc);
+  const float d = fmaf(p, sc, 1.0f);
+  return (g / d) * u;
+}
+static inline float silu_up_tail(float g, float u) { return (g / (1.f + expf(-g))) * u; }
+
+/* cpp/src/backend/cpu/ops_cpu.cpp:126-136: lanes in groups of 8 from the start
+ * of the buffer, the n % 8 tail through libm. */
+OVO_API void ovo_silu_mul_f32(float* out, const float* g, const float* u, int64_t n) {
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8)
+    for (int j = 0; j < 8; ++j) out[i + j] = silu_up_lane(g[i + j], u[i + j]);
+  for (; i < n; ++i) out[i] = silu_up_tail(g[i], u[i]);
+}
+
+/* cpp/src/backend/cpu/ops_cpu.cpp:144-198: per row and 32-k block, groups of 8
+ * from the block start use exp256, the block's kn % 8 tail uses libm. */
+OVO_API void ovo_silu_mul_quantize_u8(int64_t M, int64_t K, const float* gate, const float* up,
+                                      uint8_t* aq, float* asc) {
+  if (M <= 0 || K <= 0) return;
+  const int64_t Kb = kb_of(K), Kp = Kb * 32;
+#pragma omp parallel for schedule(static) if (M >= 32)
+  for (int64_t r = 0; r < M; ++r) {
+    const float* gr = gate + r * K;
+    const float* ur = up + r * K;
+    float v[32];
+    for (int64_t b = 0; b < Kb; ++b) {
+      const int64_t k0 = b * 32, kn = (K - k0 < 32) ? (K - k0) : 32;
+      const int64_t kv = (kn / 8) * 8;
+      int64_t i = 0;
+      for (; i < kv; ++i) v[i] = silu_up_lane(gr[k0 + i], ur[k0 + i]);
+      for (; i < kn; ++i) v[i] = silu_up_tail(gr[k0 + i], ur[k0 + i]);
+      asc[r * Kb + b] = quant_block_u8(v, kn, aq + r * Kp + k0);
+    }
+  }
+}
+
+/* Per-block int32 products, gemm.cpp:455-474: Σ u8·w over the block minus
+ * 128·Σ w, i.e. Σ q·w with q = u8 - 128 (pads are 0 in both operands).
+ * out[(m*N + n)*Kb + b]. */
+OVO_API void ovo_block_dots(int64_t M, int64_t N, int64_t K, const uint8_t* aq, const int8_t* W,
+                            int32_t* out) {
+  const int64_t Kb = kb_of(K), Kp = Kb * 32;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      const uint8_t* a = aq + m * Kp;
+      const int8_t* w = W + n * K;
+      for (int64_t b = 0; b < Kb; ++b) {
+        const int64_t k0 = b * 32, kn = (K - k0 < 32) ? (K - k0) : 32;
+        int32_t acc = 0, wsum = 0;
+        for (int64_t k = 0; k < kn; ++k) {
+          acc += (int32_t)a[k0 + k] * (int32_t)w[k0 + k];
+          wsum += w[k0 + k];
+        }
+        out[(m * N + n) * Kb + b] = acc - 128 * wsum;
+      }
+    }
+  }
+}
+
+/* gemm.cpp:432-504, one output at a time: the block epilogue, the column scale,
+ * and the separately rounded residual add.  C has leading dimension ldc. */
+OVO_API void ovo_linear_q(int64_t M, int64_t N, int64_t K, const uint8_t* aq, const float* asc,
+                          const int8_t* W, const float* wscale, float* C, int64_t ldc,
+                          int accumulate) {
+  if (M <= 0 || N <= 0 || K <= 0) return;
+  const int64_t Kb = kb_of(K), Kp = Kb * 32;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      const uint8_t* a = aq + m * Kp;
+      const int8_t* w = W + n * K;
+      float f = 0.f;
+      for (int64_t b = 0; b < Kb; ++b) {
+        const int64_t k0 = b * 32, kn = (K - k0 < 32) ? (K - k0) : 32;
+        int32_t acc = 0;
+        for (int64_t k = 0; k < kn; ++k)
+          acc += ((int32_t)a[k0 + k] - 128) * (int32_t)w[k0 + k];
+        f = fmaf((float)acc, asc[m * Kb + b], f);
+      }
+      float o = f * wscale[n];
+      if (accumulate) o = o + C[m * ldc + n];
+      C[m * ldc + n] = o;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * AVX-512 VNNI form of ovo_linear_q (identical bits; used for CPU timing).
+ *
+ * Packed weights: panels of 16 output rows; inside a panel one 64-byte group
+ * per 4 k holds byte j*4+l = W[n0+j][4g+l] (the operand shape vpdpbusd needs);
+ * wsum[b*Npad + n] = Σ_{k in block b} W[n,k] removes the +128 zero point.
+ * ---------------------------------------------------------------------- */
+static inline int64_t npad16(int64_t N) { return ((N + 15) / 16) * 16; }
+
+OVO_API int64_t ovo_packed_bytes(int64_t N, int64_t K) { return npad16(N) * kb_of(K) * 32; }
+OVO_API int64_t ovo_wsum_elems(int64_t N, int64_t K) { return npad16(N) * kb_of(K); }
+
+OVO_API void ovo_pack(int64_t N, int64_t K, const int8_t* W, int8_t* packed, int32_t* wsum) {
+  const int64_t Kb = kb_of(K), Np = npad16(N), G = Kb * 8;
+  memset(packed, 0, (size_t)(Np * Kb * 32));
+  memset(wsum, 0, sizeof(int32_t) * (size_t)(Np * Kb));
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const int64_t p = n / 16, j = n % 16;
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t g = k / 4, l = k % 4;
+      packed[(p * G + g) * 64 + j * 4 + l] = W[n * K + k];
+      wsum[(k / 32) * Np + n] += W[n * K + k];
+    }
+  }
+}
+
+OVO_API int ovo_fast_available(void) {
+#if defined(__x86_64__)
+  __builtin_cpu_init();
+  return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+         __builtin_cpu_supports("avx512vnni");
+#else
+  return 0;
+#endif
+}
+
+#if defined(__x86_64__)
+#define OVO_AVX512 __attribute__((target("avx512f,avx512bw,avx512vl,avx512vnni")))
+
+/* 4 rows x 32 columns (two panels) per call. */
+OVO_AVX512 static void tile_4x32(int64_t m0, int rows, int64_t p0, int npanels, int64_t N,
+                                 int64_t Kb, int64_t Kp, int64_t Np, const uint8_t* aq,
+                                 const float* asc, const int8_t* packed, const int32_t* wsum,
+                                 const float* wscale, float* C, int64_t ldc, int accumulate) {
+  const int64_t G = Kb * 8;
+  const uint8_t* ar[4];
+  for (int r = 0; r < 4; ++r) ar[r] = aq + (m0 + (r < rows ? r : 0)) * Kp;
+  __m512 f[4][2];
+  for (int r = 0; r < 4; ++r) f[r][0] = f[r][1] = _mm512_setzero_ps();
+  const int8_t* w0 = packed + p0 * G * 64;
+  const int8_t* w1 = packed + (p0 + (npanels > 1 ? 1 : 0)) * G * 64;
+  for (int64_t b = 0; b < Kb; ++b) {
+    __m512i c[4][2];
+    for (int r = 0; r < 4; ++r) c[r][0] = c[r][1] = _mm512_setzero_si512();
+    for (int gg = 0; gg < 8; ++gg) {
+      const int64_t g = b * 8 + gg;
+      const __m512i b0 = _mm512_loadu_si512((const void*)(w0 + g * 64));
+      const __m512i b1 = _mm512_loadu_si512((const void*)(w1 + g * 64));
+      for (int r = 0; r < 4; ++r) {
+        uint32_t a4;
+        memcpy(&a4, ar[r] + 4 * g, 4);
+        const __m512i av = _mm512_set1_epi32((int)a4);
+        c[r][0] = _mm512_dpbusd_epi32(c[r][0], av, b0);
+        c[r][1] = _mm512_dpbusd_epi32(c[r][1], av, b1);
+      }
+    }
+    for (int h = 0; h < 2; ++h) {
+      const int64_t n0 = (p0 + h) * 16;
+      if (n0 >= Np) continue;
+      const __m512i corr =
+          _mm512_slli_epi32(_mm512_loadu_si512((const void*)(wsum + b * Np + n0)), 7);
+      for (int r = 0; r < rows; ++r) {
+        const __m512 v = _mm512_cvtepi32_ps(_mm512_sub_epi32(c[r][h], corr));
+        f[r][h] = _mm512_fmadd_ps(v, _mm512_set1_ps(asc[(m0 + r) * Kb + b]), f[r][h]);
+      }
+    }
+  }
+  for (int h = 0; h < npanels; ++h) {
+    const int64_t n0 = (p0 + h) * 16;
+    const int64_t nv = (N - n0 < 16) ? (N - n0) : 16;
+    if (nv <= 0) continue;
+    const __mmask16 mk = (__mmask16)((1u << nv) - 1u);
+    const __m512 ws = _mm512_maskz_loadu_ps(mk, wscale + n0);
+    for (int r = 0; r < rows; ++r) {
+      float* cp = C + (m0 + r) * ldc + n0;
+      __m512 o = _mm512_mul_ps(f[r][h], ws);
+      if (accumulate) o = _mm512_add_ps(o, _mm512_maskz_loadu_ps(mk, cp));
+      _mm512_mask_storeu_ps(cp, mk, o);
+    }
+  }
+}
+
+OVO_AVX512 static void linear_q_packed_avx512(int64_t M, int64_t N, int64_t K,
+                                              const uint8_t* aq, const float* asc,
+                                              const int8_t* packed, const int32_t* wsum,
+                                              const float* wscale, float* C, int64_t ldc,
+                                              int accumulate) {
+  const int64_t Kb = kb_of(K), Kp = Kb * 32, Np = npad16(N);
+  const int64_t pairs = (Np / 16 + 1) / 2, rblocks = (M + 3) / 4;
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
+  for (int64_t pp = 0; pp < pairs; ++pp) {
+    for (int64_t rb = 0; rb < rblocks; ++rb) {
+      const int64_t p0 = pp * 2;
+      const int np = (p0 + 1 < Np / 16) ? 2 : 1;
+      const int64_t m0 = rb * 4;
+      const int rows = (int)((M - m0 < 4) ? (M - m0) : 4);
+      tile_4x32(m0, rows, p0, np, N, Kb, Kp, Np, aq, asc, packed, wsum, wscale, C, ldc,
+                accumulate);
+    }
+  }
+}
+#endif
+
+/* Returns 0 on success, -1 when the AVX-512 VNNI form is unavailable. */
+OVO_API int ovo_linear_q_packed(int64_t M, int64_t N, int64_t K, const uint8_t* aq,
+                                const float* asc, const int8_t* packed, const int32_t* wsum,
+                                const float* wscale, float* C, int64_t ldc, int accumulate) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+#if defined(__x86_64__)
+  if (ovo_fast_available()) {
+    linear_q_packed_avx512(M, N, K, aq, asc, packed, wsum, wscale, C, ldc, accumulate);
+    return 0;
+  }
+#endif
+  return -1;
+}
+
+OVO_API int ovo_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
