@@ -1,0 +1,146 @@
+/* ovnative_amd.h — C ABI of the MI355X (gfx950) int8-nk quantized-linear path.
+ *
+ * This is the drop-in boundary for OVNative's quantized linear layers.  Each
+ * entry point replaces one function of the reference's CPU operator API
+ * (cpp/include/ovnative/ov_gemm.h, namespace ov) with the same argument
+ * meaning, except that every buffer is DEVICE memory and every call is
+ * enqueued on a caller-supplied HIP stream (`stream` = hipStream_t, NULL for
+ * the null stream).  Calls are asynchronous with respect to the host.
+ *
+ * Status codes are the reference C ABI's (cpp/include/ovnative/ovnative.h:18-23).
+ * Errors never throw across this boundary; a failing call returns a negative
+ * status and leaves a message for ovh_last_error() on the calling thread.
+ * Degenerate sizes (M, N or K <= 0) return OV_OK without doing anything, as the
+ * reference does (cpp/src/backend/cpu/gemm.cpp:761).
+ *
+ * Activation format on the device.  The reference quantises activations per
+ * row and 32-k block to u8 = q + 128 (cpp/src/backend/cpu/gemm.cpp:379-430).
+ * Here the same q is stored signed: aq is int8 [M, Kp], Kp = 32*ceil(K/32),
+ * with aq_s8 = aq_u8 - 128 for every real k and 0 in the K-tail padding (the
+ * reference pads u8 with 0; the matching weight bytes are 0 either way), and
+ * asc is fp32 [M, ceil(K/32)], identical to the reference's scales.
+ *
+ * Weight format on the device.  OVW1 int8 weights carry one fp32 scale per
+ * output channel (tools/convert_weights.py:130-135).  ovh_weight_upload() takes
+ * either OVW1 layout (0 = [N, K] "nk", 1 = [K, N] "kn"; the integers and scales
+ * are the same, cpp/src/model/mat.cpp:69-106) and builds the device layout the
+ * kernels read; the handle owns that memory.
+ *
+ * Threading: a handle may be used from any thread; calls that write the same
+ * output buffer must be ordered by the caller (same stream), as with the
+ * reference's synchronous API.
+ */
+#ifndef OVNATIVE_AMD_H
+#define OVNATIVE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility push(default)
+#endif
+
+#define OVH_ABI_VERSION 1
+
+/* Status codes: same values as cpp/include/ovnative/ovnative.h:18-23. */
+#ifndef OV_OK
+#define OV_OK 0
+#define OV_ERR_INVALID_ARG (-1)
+#define OV_ERR_IO (-2)
+#define OV_ERR_NOT_IMPLEMENTED (-3)
+#define OV_ERR_INTERNAL (-4)
+#endif
+
+typedef struct OvhWeight OvhWeight;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* ovh_last_error(void);
+
+/* ABI version and the device the library runs on, e.g. "hip:gfx950 (256 CUs)".
+ * Plays the role of ov_engine_backend() (cpp/include/ovnative/ovnative.h:49)
+ * and cpu_kernel_name() (cpp/include/ovnative/ov_gemm.h:122). */
+int ovh_abi_version(void);
+int ovh_backend_name(char* buf, size_t len);
+
+/* Activation buffer sizes; replace s8_nk_quant_bytes / s8_nk_quant_scales
+ * (cpp/include/ovnative/ov_gemm.h:95-96, gemm.cpp:623-631). */
+int64_t ovh_quant_bytes(int64_t M, int64_t K);
+int64_t ovh_quant_scales(int64_t M, int64_t K);
+
+/* ---- weights --------------------------------------------------------------
+ * Replaces the load-time repack s8_nk_pack (ov_gemm.h:60-63, gemm.cpp:584-621)
+ * and make_linear's layout dispatch (mat.cpp:69-106).  `q` is int8 in OVW1
+ * layout `layout` (0: [N,K], 1: [K,N]); `scale` has N floats.  Host pointers
+ * for ovh_weight_upload, device pointers for ovh_weight_from_device.  The
+ * handle's memory is allocated here and freed by ovh_weight_free. */
+int ovh_weight_upload(int64_t N, int64_t K, const int8_t* q, const float* scale, int layout,
+                      void* stream, OvhWeight** out);
+int ovh_weight_from_device(int64_t N, int64_t K, const int8_t* q, const float* scale,
+                           int layout, void* stream, OvhWeight** out);
+/* Concatenate weights with equal K along N (q/k/v -> qkv, gate/up -> gate_up);
+ * replaces combine_packed (cpp/src/model/lm.cpp:57-94).  Each part's N must be
+ * a positive multiple of 64, as the reference requires. */
+int ovh_weight_concat(const OvhWeight* const* parts, int n_parts, void* stream, OvhWeight** out);
+void ovh_weight_free(OvhWeight* w);
+int64_t ovh_weight_n(const OvhWeight* w);
+int64_t ovh_weight_k(const OvhWeight* w);
+/* Copy the weight back as OVW1 layout-0 int8 [N,K] + fp32 scales (device
+ * pointers); used by tests to prove the layout transform is lossless. */
+int ovh_weight_download(const OvhWeight* w, int8_t* q_nk, float* scale, void* stream);
+
+/* ---- activation quantisers ------------------------------------------------ */
+/* s8_nk_quantize (ov_gemm.h:97, gemm.cpp:709-720 -> quantize_a_u8 :379-430).
+ * A fp32 [M,K] -> aq int8 [M,Kp], asc fp32 [M,Kb]. */
+int ovh_s8_nk_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
+                       void* stream);
+/* rmsnorm_quantize_f32 (ov_gemm.h:118-119, gemm.cpp:722-756 -> :638-707):
+ * xn = (x * 1/sqrt(mean(x^2)+eps)) * w, quantised without materialising xn. */
+int ovh_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w, float eps,
+                         int8_t* aq, float* asc, void* stream);
+/* silu_mul_quantize_f32 (ov_gemm.h:84-85, ops_cpu.cpp:1138-1168 -> :144-198):
+ * silu(gate)*up quantised per 32-k block. */
+int ovh_silu_mul_quantize(int64_t M, int64_t K, const float* gate, const float* up, int8_t* aq,
+                          float* asc, void* stream);
+
+/* ---- GEMM ------------------------------------------------------------------
+ * C[m, n] = wscale[n] * sum_b fma-chain(float(acc_b[m,n]) * asc[m,b]) with
+ * acc_b the exact int32 dot product of block b; bit-identical to the reference's
+ * epilogue (gemm.cpp:469-502).  C has leading dimension ldc >= N.
+ *
+ * linear_s8_nk_packed_q (ov_gemm.h:98-100, gemm.cpp:758-774): accumulate = 0.
+ * linear_s8_nk_packed_q_add (ov_gemm.h:78-80, gemm.cpp:847-862): accumulate = 1,
+ * C = C + P with P rounded first (the reference's "keep mul/add separate"). */
+int ovh_linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
+                 int64_t ldc, int accumulate, void* stream);
+/* linear_s8_nk_packed_q_sliced (ov_gemm.h:105-111, gemm.cpp:776-827): one launch
+ * over a concatenated weight, slice s (N = slice_n[s], a positive multiple of
+ * 64, summing to the weight's N) written to slice_c[s] with leading dimension
+ * slice_n[s].  Invalid slices -> OV_ERR_INVALID_ARG (the reference throws
+ * std::invalid_argument). */
+int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                        const int64_t* slice_n, float* const* slice_c, int n_slices,
+                        void* stream);
+/* linear_s8_nk_packed / _packed_add (ov_gemm.h:67-75, gemm.cpp:829-845, :864-882):
+ * quantise A (fp32 [M,K]) into a library-owned workspace, then ovh_linear_q. */
+int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+               int accumulate, void* stream);
+
+/* Debug: the exact int32 dot product of every (m, n, block) computed by the
+ * same MFMA code path as ovh_linear_q; out is int32 [M, N, Kb].  The reference
+ * keeps these in registers (gemm.cpp:455-474); this exposes them for the
+ * bit-exactness check. */
+int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream);
+
+#if defined(__GNUC__) || defined(__clang__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OVNATIVE_AMD_H */

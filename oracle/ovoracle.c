@@ -56,11 +56,21 @@
 
 #define OVO_API __attribute__((visibility("default")))
 
+/* OVO_PLANT selects a deliberate mistake, for tests/test_oracle.py to prove the
+ * golden vectors catch it (never set in a normal build):
+ *   1 unfused exp256 range reduction   2 sequential RMSNorm sum
+ *   3 unfused block epilogue           4 truncating quantiser
+ *   5 wrong zero point (127)           6 weight scale floor skipped */
+#ifndef OVO_PLANT
+#define OVO_PLANT 0
+#endif
+
 static inline int64_t kb_of(int64_t K) { return (K + 31) / 32; }
 
 /* cvtps_epi32 semantics in round-to-nearest-even mode. */
 static inline int32_t cvt_rne_i32(float x) {
   if (!(fabsf(x) < 2147483648.0f)) return INT32_MIN;
+  if (OVO_PLANT == 4) return (int32_t)x;
   return (int32_t)nearbyintf(x);
 }
 
@@ -101,7 +111,7 @@ OVO_API void ovo_quantize_weight_rows(int64_t N, int64_t K, const float* W, int8
       amax = a > amax ? a : amax;
     }
     float s = amax / 127.0f;
-    s = s > floor_scale ? s : floor_scale;
+    if (OVO_PLANT != 6) s = s > floor_scale ? s : floor_scale;
     scale[n] = s;
     for (int64_t k = 0; k < K; ++k) {
       float r = rintf(row[k] / s);
@@ -130,6 +140,11 @@ OVO_API void ovo_quantize_u8(int64_t M, int64_t K, const float* A, uint8_t* aq, 
 static float rms_scale(const float* row, int64_t cols, float eps) {
   float lanes[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int64_t i = 0;
+  if (OVO_PLANT == 2) {
+    float seq = 0.f;
+    for (; i < cols; ++i) seq = fmaf(row[i], row[i], seq);
+    return 1.f / sqrtf(seq / (float)cols + eps);
+  }
   for (; i + 8 <= cols; i += 8)
     for (int j = 0; j < 8; ++j) lanes[j] = fmaf(row[i + j], row[i + j], lanes[j]);
   float sum = lanes[0];
@@ -188,7 +203,8 @@ static inline void exp256_parts(float x, float* p_out, float* sc_out) {
   x = x < 88.0f ? x : 88.0f; /* minps returns the second operand on NaN */
   x = x > -87.0f ? x : -87.0f;
   const float n = nearbyintf(x * 1.4426950408889634f);
-  const float r = fmaf(-n, 0.6931471805599453f, x);
+  const float r = OVO_PLANT == 1 ? x - n * 0.6931471805599453f
+                                 : fmaf(-n, 0.6931471805599453f, x);
   float p = 1.0f / 720;
   p = fmaf(p, r, 1.0f / 120);
   p = fmaf(p, r, 1.0f / 24);
@@ -268,7 +284,7 @@ OVO_API void ovo_block_dots(int64_t M, int64_t N, int64_t K, const uint8_t* aq, 
           acc += (int32_t)a[k0 + k] * (int32_t)w[k0 + k];
           wsum += w[k0 + k];
         }
-        out[(m * N + n) * Kb + b] = acc - 128 * wsum;
+        out[(m * N + n) * Kb + b] = acc - (OVO_PLANT == 5 ? 127 : 128) * wsum;
       }
     }
   }
@@ -291,8 +307,9 @@ OVO_API void ovo_linear_q(int64_t M, int64_t N, int64_t K, const uint8_t* aq, co
         const int64_t k0 = b * 32, kn = (K - k0 < 32) ? (K - k0) : 32;
         int32_t acc = 0;
         for (int64_t k = 0; k < kn; ++k)
-          acc += ((int32_t)a[k0 + k] - 128) * (int32_t)w[k0 + k];
-        f = fmaf((float)acc, asc[m * Kb + b], f);
+          acc += ((int32_t)a[k0 + k] - (OVO_PLANT == 5 ? 127 : 128)) * (int32_t)w[k0 + k];
+        f = OVO_PLANT == 3 ? f + (float)acc * asc[m * Kb + b]
+                           : fmaf((float)acc, asc[m * Kb + b], f);
       }
       float o = f * wscale[n];
       if (accumulate) o = o + C[m * ldc + n];

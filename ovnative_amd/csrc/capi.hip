@@ -1,0 +1,340 @@
+// extern "C" entry points of libovnative_amd.so (declared in include/ovnative_amd.h).
+//
+// Argument checking and error reporting follow the reference's operator API
+// (cpp/include/ovnative/ov_gemm.h): degenerate sizes are a silent no-op, bad
+// slice widths are an invalid argument, and a failure never escapes as an
+// exception — it becomes a status code plus a per-thread message.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/ovnative_amd.h"
+#include "gemm.h"
+#include "ovh_common.h"
+#include "quant.h"
+
+struct OvhWeight {
+  ovh::DeviceWeight w;
+};
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const std::string& msg) {
+  t_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(OV_ERR_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define OVH_HIP(expr, what)                      \
+  do {                                           \
+    const hipError_t e_ = (expr);                \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int new_weight(int64_t N, int64_t K, OvhWeight** out) {
+  auto* h = new (std::nothrow) OvhWeight();
+  if (!h) return fail(OV_ERR_INTERNAL, "out of host memory");
+  ovh::DeviceWeight& w = h->w;
+  w.N = N;
+  w.K = K;
+  w.Kb = ovh::kb_of(K);
+  w.Kp = w.Kb * 32;
+  w.Npad = (N + ovh::kRowPad - 1) / ovh::kRowPad * ovh::kRowPad;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w.q), (size_t)(w.Npad * w.Kp));
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&w.scale), sizeof(float) * (size_t)w.Npad);
+  if (e != hipSuccess) {
+    if (w.q) (void)hipFree(w.q);
+    delete h;
+    return hip_fail(e, "hipMalloc(weight)");
+  }
+  *out = h;
+  return OV_OK;
+}
+
+int check_gemm_operands(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w) {
+  if (!w) return fail(OV_ERR_INVALID_ARG, "weight handle is null");
+  if (M > 0x7fffffff || w->w.N > 0x7fffffff)
+    return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
+  if (!aq || !asc) return fail(OV_ERR_INVALID_ARG, "aq/asc must be device pointers");
+  if (!aligned16(aq)) return fail(OV_ERR_INVALID_ARG, "aq must be 16-byte aligned");
+  return OV_OK;
+}
+
+ovh::GemmArgs base_args(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w) {
+  ovh::GemmArgs a;
+  a.M = (int)M;
+  a.N = (int)w->w.N;
+  a.Kb = (int)w->w.Kb;
+  a.Kp = w->w.Kp;
+  a.aq = aq;
+  a.asc = asc;
+  a.W = w->w.q;
+  a.ws = w->w.scale;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ovh_last_error(void) { return t_err.c_str(); }
+
+int ovh_abi_version(void) { return OVH_ABI_VERSION; }
+
+int ovh_backend_name(char* buf, size_t len) {
+  int dev = 0;
+  OVH_HIP(hipGetDevice(&dev), "hipGetDevice");
+  hipDeviceProp_t p;
+  OVH_HIP(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+  if (buf && len) std::snprintf(buf, len, "hip:%s (%d CUs)", p.gcnArchName, p.multiProcessorCount);
+  return OV_OK;
+}
+
+int64_t ovh_quant_bytes(int64_t M, int64_t K) {
+  return (M <= 0 || K <= 0) ? 0 : M * ovh::kb_of(K) * 32;
+}
+int64_t ovh_quant_scales(int64_t M, int64_t K) {
+  return (M <= 0 || K <= 0) ? 0 : M * ovh::kb_of(K);
+}
+
+// ---- weights ----------------------------------------------------------------
+
+int ovh_weight_from_device(int64_t N, int64_t K, const int8_t* q, const float* scale, int layout,
+                           void* stream, OvhWeight** out) {
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  if (N <= 0 || K <= 0) return fail(OV_ERR_INVALID_ARG, "weight dims must be positive");
+  if (layout != 0 && layout != 1) return fail(OV_ERR_INVALID_ARG, "layout must be 0 (nk) or 1 (kn)");
+  if (!q || !scale) return fail(OV_ERR_INVALID_ARG, "q/scale are null");
+  OvhWeight* h = nullptr;
+  const int rc = new_weight(N, K, &h);
+  if (rc != OV_OK) return rc;
+  const hipError_t e = ovh::launch_weight_layout(N, K, q, layout, scale, h->w, as_stream(stream));
+  if (e != hipSuccess) {
+    ovh_weight_free(h);
+    return hip_fail(e, "weight layout");
+  }
+  *out = h;
+  return OV_OK;
+}
+
+int ovh_weight_upload(int64_t N, int64_t K, const int8_t* q, const float* scale, int layout,
+                      void* stream, OvhWeight** out) {
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  if (N <= 0 || K <= 0) return fail(OV_ERR_INVALID_ARG, "weight dims must be positive");
+  if (!q || !scale) return fail(OV_ERR_INVALID_ARG, "q/scale are null");
+  int8_t* dq = nullptr;
+  float* ds = nullptr;
+  const hipStream_t st = as_stream(stream);
+  OVH_HIP(hipMalloc(reinterpret_cast<void**>(&dq), (size_t)(N * K)), "hipMalloc(staging)");
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&ds), sizeof(float) * (size_t)N);
+  if (e == hipSuccess) e = hipMemcpyAsync(dq, q, (size_t)(N * K), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(ds, scale, sizeof(float) * (size_t)N, hipMemcpyHostToDevice, st);
+  int rc = OV_OK;
+  if (e != hipSuccess) {
+    rc = hip_fail(e, "weight upload");
+  } else {
+    rc = ovh_weight_from_device(N, K, dq, ds, layout, stream, out);
+    if (rc == OV_OK) {
+      e = hipStreamSynchronize(st);  // staging buffers are freed below
+      if (e != hipSuccess) {
+        ovh_weight_free(*out);
+        *out = nullptr;
+        rc = hip_fail(e, "weight upload sync");
+      }
+    }
+  }
+  (void)hipFree(dq);
+  if (ds) (void)hipFree(ds);
+  return rc;
+}
+
+int ovh_weight_concat(const OvhWeight* const* parts, int n_parts, void* stream, OvhWeight** out) {
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  if (!parts || n_parts <= 0) return fail(OV_ERR_INVALID_ARG, "no parts");
+  int64_t N = 0;
+  const int64_t K = parts[0] ? parts[0]->w.K : 0;
+  for (int i = 0; i < n_parts; ++i) {
+    if (!parts[i] || parts[i]->w.K != K || parts[i]->w.N % 64 != 0)
+      return fail(OV_ERR_INVALID_ARG, "concat: parts need equal K and N a multiple of 64");
+    N += parts[i]->w.N;
+  }
+  OvhWeight* h = nullptr;
+  const int rc = new_weight(N, K, &h);
+  if (rc != OV_OK) return rc;
+  const hipStream_t st = as_stream(stream);
+  ovh::DeviceWeight& w = h->w;
+  hipError_t e = hipSuccess;
+  int64_t row = 0;
+  for (int i = 0; i < n_parts && e == hipSuccess; ++i) {
+    const ovh::DeviceWeight& p = parts[i]->w;
+    e = hipMemcpyAsync(w.q + row * w.Kp, p.q, (size_t)(p.N * p.Kp), hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(w.scale + row, p.scale, sizeof(float) * (size_t)p.N,
+                         hipMemcpyDeviceToDevice, st);
+    row += p.N;
+  }
+  if (e == hipSuccess && w.Npad > N) {
+    e = hipMemsetAsync(w.q + N * w.Kp, 0, (size_t)((w.Npad - N) * w.Kp), st);
+    if (e == hipSuccess)
+      e = hipMemsetAsync(w.scale + N, 0, sizeof(float) * (size_t)(w.Npad - N), st);
+  }
+  if (e != hipSuccess) {
+    ovh_weight_free(h);
+    return hip_fail(e, "weight concat");
+  }
+  *out = h;
+  return OV_OK;
+}
+
+void ovh_weight_free(OvhWeight* h) {
+  if (!h) return;
+  if (h->w.q) (void)hipFree(h->w.q);
+  if (h->w.scale) (void)hipFree(h->w.scale);
+  delete h;
+}
+
+int64_t ovh_weight_n(const OvhWeight* w) { return w ? w->w.N : 0; }
+int64_t ovh_weight_k(const OvhWeight* w) { return w ? w->w.K : 0; }
+
+int ovh_weight_download(const OvhWeight* w, int8_t* q_nk, float* scale, void* stream) {
+  if (!w || !q_nk || !scale) return fail(OV_ERR_INVALID_ARG, "null argument");
+  const hipStream_t st = as_stream(stream);
+  hipError_t e = ovh::launch_weight_to_nk(w->w, q_nk, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(scale, w->w.scale, sizeof(float) * (size_t)w->w.N,
+                       hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return hip_fail(e, "weight download");
+  return OV_OK;
+}
+
+// ---- quantisers ---------------------------------------------------------------
+
+int ovh_s8_nk_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
+                       void* stream) {
+  if (M <= 0 || K <= 0) return OV_OK;
+  if (!A || !aq || !asc) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (((uintptr_t)aq & 3u) != 0) return fail(OV_ERR_INVALID_ARG, "aq must be 4-byte aligned");
+  OVH_HIP(ovh::launch_quantize(M, K, A, aq, asc, as_stream(stream)), "quantize launch");
+  return OV_OK;
+}
+
+int ovh_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w, float eps,
+                         int8_t* aq, float* asc, void* stream) {
+  if (rows <= 0 || cols <= 0) return OV_OK;
+  if (!x || !w || !aq || !asc) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (((uintptr_t)aq & 3u) != 0) return fail(OV_ERR_INVALID_ARG, "aq must be 4-byte aligned");
+  if (ovh::rmsnorm_quantize_smem(cols) > 160 * 1024)
+    return fail(OV_ERR_INVALID_ARG, "rmsnorm_quantize: cols too large for one LDS row stage");
+  OVH_HIP(ovh::launch_rmsnorm_quantize(rows, cols, x, w, eps, aq, asc, as_stream(stream)),
+          "rmsnorm_quantize launch");
+  return OV_OK;
+}
+
+int ovh_silu_mul_quantize(int64_t M, int64_t K, const float* gate, const float* up, int8_t* aq,
+                          float* asc, void* stream) {
+  if (M <= 0 || K <= 0) return OV_OK;
+  if (!gate || !up || !aq || !asc) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (((uintptr_t)aq & 3u) != 0) return fail(OV_ERR_INVALID_ARG, "aq must be 4-byte aligned");
+  OVH_HIP(ovh::launch_silu_mul_quantize(M, K, gate, up, aq, asc, as_stream(stream)),
+          "silu_mul_quantize launch");
+  return OV_OK;
+}
+
+// ---- GEMM -----------------------------------------------------------------------
+
+int ovh_linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
+                 int64_t ldc, int accumulate, void* stream) {
+  if (M <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, asc, w);
+  if (rc != OV_OK) return rc;
+  if (!C) return fail(OV_ERR_INVALID_ARG, "C is null");
+  if (ldc < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldc < N");
+  ovh::GemmArgs a = base_args(M, aq, asc, w);
+  a.nslices = 1;
+  a.start[0] = 0;
+  a.start[1] = (int)w->w.N;
+  a.out[0] = C;
+  a.ld[0] = ldc;
+  OVH_HIP(ovh::launch_gemm(a, accumulate ? ovh::kAccumulate : ovh::kStore, as_stream(stream)),
+          "gemm launch");
+  return OV_OK;
+}
+
+int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                        const int64_t* slice_n, float* const* slice_c, int n_slices,
+                        void* stream) {
+  if (M <= 0 || n_slices <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, asc, w);
+  if (rc != OV_OK) return rc;
+  if (!slice_n || !slice_c) return fail(OV_ERR_INVALID_ARG, "slices are null");
+  if (n_slices > ovh::kMaxSlices)
+    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: at most 8 slices");
+  ovh::GemmArgs a = base_args(M, aq, asc, w);
+  int64_t total = 0;
+  a.nslices = n_slices;
+  for (int s = 0; s < n_slices; ++s) {
+    if (slice_n[s] <= 0 || slice_n[s] % 64 != 0 || !slice_c[s])
+      return fail(OV_ERR_INVALID_ARG, "sliced GEMM: each slice N must be a positive multiple of 64");
+    a.start[s] = (int)total;
+    a.out[s] = slice_c[s];
+    a.ld[s] = slice_n[s];
+    total += slice_n[s];
+  }
+  if (total != w->w.N)
+    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: slice widths must sum to the weight's N");
+  a.start[n_slices] = (int)total;
+  OVH_HIP(ovh::launch_gemm(a, ovh::kStore, as_stream(stream)), "gemm launch");
+  return OV_OK;
+}
+
+int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+               int accumulate, void* stream) {
+  if (M <= 0) return OV_OK;
+  if (!w || !A) return fail(OV_ERR_INVALID_ARG, "null argument");
+  const hipStream_t st = as_stream(stream);
+  int8_t* aq = nullptr;
+  float* asc = nullptr;
+  OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(&aq), (size_t)(M * w->w.Kp), st),
+          "hipMallocAsync(aq)");
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&asc),
+                                sizeof(float) * (size_t)(M * w->w.Kb), st);
+  int rc = OV_OK;
+  if (e != hipSuccess) {
+    rc = hip_fail(e, "hipMallocAsync(asc)");
+  } else {
+    rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
+    if (rc == OV_OK) rc = ovh_linear_q(M, aq, asc, w, C, ldc, accumulate, stream);
+  }
+  (void)hipFreeAsync(aq, st);
+  if (asc) (void)hipFreeAsync(asc, st);
+  return rc;
+}
+
+int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream) {
+  if (M <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, reinterpret_cast<const float*>(aq), w);
+  if (rc != OV_OK) return rc;
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  ovh::GemmArgs a = base_args(M, aq, nullptr, w);
+  a.asc = nullptr;
+  a.start[1] = (int)w->w.N;
+  a.dump = out;
+  OVH_HIP(ovh::launch_gemm(a, ovh::kDumpBlocks, as_stream(stream)), "gemm launch");
+  return OV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,43 @@
+// Launchers for the int8 MFMA GEMM (gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ovh {
+
+constexpr int kMaxSlices = 8;
+// Device weights are padded to a multiple of this many output rows, so every
+// N-tile the kernels use (32..128 rows) reads in-bounds rows and zero scales.
+constexpr int kRowPad = 128;
+
+enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2 };
+
+// Device weight: int8 [Npad][Kp] row-major (row n = output channel n, K tail
+// and rows >= N zero) and fp32 scale [Npad] (0 beyond N).
+struct DeviceWeight {
+  int64_t N = 0, K = 0, Npad = 0, Kb = 0, Kp = 0;
+  int8_t* q = nullptr;
+  float* scale = nullptr;
+};
+
+struct GemmArgs {
+  int M = 0, N = 0, Kb = 0;
+  int64_t Kp = 0;
+  const int8_t* aq = nullptr;   // [M][Kp]
+  const float* asc = nullptr;   // [M][Kb]
+  const int8_t* W = nullptr;    // [Npad][Kp]
+  const float* ws = nullptr;    // [Npad]
+  int nslices = 1;
+  int start[kMaxSlices + 1] = {0};
+  float* out[kMaxSlices] = {nullptr};
+  int64_t ld[kMaxSlices] = {0};
+  int32_t* dump = nullptr;      // [M][N][Kb] in kDumpBlocks mode
+};
+
+hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);
+hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
+                                const float* scale_src, DeviceWeight& dst, hipStream_t st);
+hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st);
+
+}  // namespace ovh

@@ -1,0 +1,66 @@
+// Shared device helpers for the gfx950 int8-nk kernels.
+//
+// All kernels are built with -ffp-contract=off: every fused multiply-add below
+// is an explicit fmaf(), every other product and sum is rounded on its own, so
+// the order of roundings is the one written here and nothing else.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ovh {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBlockK = 32;  // activation quantisation block (k values)
+
+__host__ __device__ inline int64_t kb_of(int64_t K) { return (K + 31) / 32; }
+
+// q = clamp(RNE(v*inv), -127, 127), where a product that x86 cvtps_epi32 cannot
+// represent (NaN, |x| >= 2^31) becomes INT_MIN and so clamps to -127, as in the
+// reference quantiser (cpp/src/backend/cpu/gemm.cpp:412-415).
+__device__ __forceinline__ int quant_q(float v, float inv) {
+  const float x = __fmul_rn(v, inv);
+  if (!(fabsf(x) < 2147483648.0f)) return -127;
+  const float r = rintf(x);
+  return (int)fminf(fmaxf(r, -127.f), 127.f);
+}
+
+// Correctly rounded fp32 square root (what x86 sqrtss returns).  v_sqrt_f32 alone
+// is a 1-ulp approximation; the f64 square root is expanded to a correctly
+// rounded sequence, and rounding a correctly rounded 53-bit root to 24 bits is
+// again correctly rounded (53 >= 2*24 + 2, so the double rounding is innocuous).
+__device__ __forceinline__ float sqrt_rn(float x) { return (float)__dsqrt_rn((double)x); }
+
+// Max over the 8 lanes of an aligned 8-lane group (one 32-k block, 4 values per lane).
+__device__ __forceinline__ float group8_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 1, 8));
+  v = fmaxf(v, __shfl_xor(v, 2, 8));
+  v = fmaxf(v, __shfl_xor(v, 4, 8));
+  return v;
+}
+
+// One 32-k block spread over an 8-lane group, 4 values per lane: computes the
+// block's amax, packs this lane's 4 int8 codes (0 for invalid slots, i.e. the
+// K-tail padding) into *codes and returns the block scale amax/127.
+__device__ __forceinline__ float quant_block_lane(const float v[4], int nvalid, uint32_t* codes) {
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i < nvalid) a = fmaxf(a, fabsf(v[i]));
+  const float amax = group8_max(a);
+  const float inv = amax > 0.f ? __fdiv_rn(127.0f, amax) : 0.f;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = i < nvalid ? quant_q(v[i], inv) : 0;
+    packed |= (uint32_t)(uint8_t)(int8_t)q << (8 * i);
+  }
+  *codes = packed;
+  return __fdiv_rn(amax, 127.0f);
+}
+
+}  // namespace ovh

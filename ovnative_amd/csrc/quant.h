@@ -1,0 +1,17 @@
+// Launchers for the activation quantisers (quant.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ovh {
+
+hipError_t launch_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
+                           hipStream_t st);
+hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
+                                   float eps, int8_t* aq, float* asc, hipStream_t st);
+size_t rmsnorm_quantize_smem(int64_t cols);
+hipError_t launch_silu_mul_quantize(int64_t M, int64_t K, const float* g, const float* u,
+                                    int8_t* aq, float* asc, hipStream_t st);
+
+}  // namespace ovh

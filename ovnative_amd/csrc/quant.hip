@@ -1,0 +1,241 @@
+// Activation quantisers for the gfx950 int8-nk path.
+//
+// Every kernel maps one 32-k block onto an aligned group of 8 lanes holding 4
+// consecutive values each, so a wavefront covers 8 blocks = 1 KiB of fp32 in
+// one coalesced pass; the block amax is an 8-lane butterfly.  Outputs: int8
+// codes q (signed; the reference's u8 byte is q + 128) and one fp32 scale per
+// block, bit-identical to the reference's bytes.
+#include "ovh_common.h"
+#include "quant.h"
+
+namespace ovh {
+
+// ---------------------------------------------------------------------------
+// s8_nk_quantize: cpp/src/backend/cpu/gemm.cpp:379-430 (quantize_a_u8).
+template <bool VEC4>
+__global__ __launch_bounds__(256) void quantize_kernel(int64_t M, int64_t K, int64_t Kb,
+                                                       const float* __restrict__ A,
+                                                       int8_t* __restrict__ aq,
+                                                       float* __restrict__ asc) {
+  const int64_t g = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  if (g >= M * Kb) return;  // the whole 8-lane group leaves together
+  const int64_t m = g / Kb, b = g - m * Kb;
+  const int64_t k0 = b * 32 + sub * 4;
+  const int64_t rem = K - k0;
+  const int nvalid = rem >= 4 ? 4 : (rem > 0 ? (int)rem : 0);
+  const float* row = A + m * K;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (VEC4 && nvalid == 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + k0);
+    v[0] = x[0]; v[1] = x[1]; v[2] = x[2]; v[3] = x[3];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nvalid) v[i] = row[k0 + i];
+  }
+  uint32_t codes;
+  const float s = quant_block_lane(v, nvalid, &codes);
+  *reinterpret_cast<uint32_t*>(aq + m * Kb * 32 + b * 32 + sub * 4) = codes;
+  if (sub == 0) asc[m * Kb + b] = s;
+}
+
+// ---------------------------------------------------------------------------
+// rmsnorm_quantize_f32: cpp/src/backend/cpu/gemm.cpp:638-707.
+//
+// The row's 1/rms must be the reference's bits, so the sum of squares follows
+// its order exactly: eight fma chains (element i feeds chain i%8, increasing i),
+// summed chain 0..7 left to right, then the cols%8 tail as the reference binary
+// computes it (4 rounded squares added in order when >= 4 remain, the rest
+// fused).  Each chain is a sequential dependence of cols/8 fmas; one wavefront
+// per row stages the row in LDS and lanes 0..7 run the chains.
+constexpr int kRmsRowsPerBlock = 4;
+
+__global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int64_t cols,
+                                                               int64_t Kb,
+                                                               const float* __restrict__ x,
+                                                               const float* __restrict__ w,
+                                                               float eps,
+                                                               int8_t* __restrict__ aq,
+                                                               float* __restrict__ asc,
+                                                               bool vec4) {
+  extern __shared__ float smem[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * kRmsRowsPerBlock + wave;
+  const bool active = r < rows;  // every wave still reaches the barriers
+  float* xs = smem + (int64_t)wave * (cols + 8);
+  float* part = xs + cols;  // 8 partial sums
+  const float* row = x + (active ? r : 0) * cols;
+  if (active) {
+    if (vec4) {
+      for (int64_t i = lane * 4; i < cols; i += 256) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(row + i);
+        xs[i] = v[0]; xs[i + 1] = v[1]; xs[i + 2] = v[2]; xs[i + 3] = v[3];
+      }
+    } else {
+      for (int64_t i = lane; i < cols; i += 64) xs[i] = row[i];
+    }
+  }
+  __syncthreads();
+  const int64_t nfull = (cols / 8) * 8;
+  if (active && lane < 8) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int64_t i = lane; i < nfull; i += 8) acc = fmaf(xs[i], xs[i], acc);
+    part[lane] = acc;
+  }
+  __syncthreads();
+  if (!active) return;
+  float sum = part[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) sum = __fadd_rn(sum, part[j]);
+  const int64_t t = cols - nfull;
+  int64_t j = 0;
+  if (t >= 4)
+    for (; j < 4; ++j) sum = __fadd_rn(sum, __fmul_rn(xs[nfull + j], xs[nfull + j]));
+  for (; j < t; ++j) sum = fmaf(xs[nfull + j], xs[nfull + j], sum);
+  const float scale =
+      __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
+
+  // Quantise: 8 blocks per pass, 8 lanes per block; the pass count is uniform
+  // across the wavefront so the 8-lane butterflies always see their partners.
+  const int grp = lane >> 3, sub = lane & 7;
+  int8_t* qrow = aq + r * Kb * 32;
+  for (int64_t b0 = 0; b0 < Kb; b0 += 8) {
+    const int64_t b = b0 + grp;
+    const int64_t k0 = b * 32 + sub * 4;
+    const int64_t rem = b < Kb ? cols - k0 : 0;
+    const int nvalid = rem >= 4 ? 4 : (rem > 0 ? (int)rem : 0);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nvalid) v[i] = __fmul_rn(__fmul_rn(xs[k0 + i], scale), w[k0 + i]);
+    uint32_t codes;
+    const float s = quant_block_lane(v, nvalid, &codes);
+    if (b < Kb) {
+      *reinterpret_cast<uint32_t*>(qrow + b * 32 + sub * 4) = codes;
+      if (sub == 0) asc[r * Kb + b] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// silu_mul_quantize_f32: cpp/src/backend/cpu/ops_cpu.cpp:144-198.
+//
+// Inside a block, the groups of 8 from the block start go through the
+// reference's exp256 lane arithmetic (ops_cpu.cpp:75-92 as its GCC build
+// compiles it: the range reduction x - n*ln2 and the final "1 + p*2^n" are
+// fused); the block's kn%8 tail goes through libm expf in the reference, here
+// through a double-precision exp rounded once to float (glibc's expf is within
+// 0.502 ulp, so the two can differ for inputs whose exp lies within ~0.002 ulp
+// of a rounding midpoint).
+__device__ __forceinline__ float silu_up_lane(float g, float u) {
+  float x = __fsub_rn(0.0f, g);
+  x = fminf(x, 88.0f);   // minps(x, 88) yields 88 for NaN, as fminf does
+  x = fmaxf(x, -87.0f);
+  const float n = rintf(__fmul_rn(x, 1.4426950408889634f));
+  const float r = fmaf(-n, 0.6931471805599453f, x);
+  float p = 1.0f / 720;
+  p = fmaf(p, r, 1.0f / 120);
+  p = fmaf(p, r, 1.0f / 24);
+  p = fmaf(p, r, 1.0f / 6);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const float sc = __int_as_float((ni + 127) << 23);
+  const float d = fmaf(p, sc, 1.0f);
+  return __fmul_rn(__fdiv_rn(g, d), u);
+}
+
+__device__ __forceinline__ float silu_up_tail(float g, float u) {
+  const float e = (float)exp(-(double)g);
+  return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.f, e)), u);
+}
+
+template <bool VEC4>
+__global__ __launch_bounds__(256) void silu_mul_quantize_kernel(
+    int64_t M, int64_t K, int64_t Kb, const float* __restrict__ gate,
+    const float* __restrict__ up, int8_t* __restrict__ aq, float* __restrict__ asc) {
+  const int64_t gi = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  if (gi >= M * Kb) return;
+  const int64_t m = gi / Kb, b = gi - m * Kb;
+  const int64_t kblk = b * 32, k0 = kblk + sub * 4;
+  const int64_t kn = (K - kblk < 32) ? (K - kblk) : 32;
+  const int64_t kv = (kn / 8) * 8;  // exp256 lanes; [kv, kn) is the libm tail
+  const int64_t rem = K - k0;
+  const int nvalid = rem >= 4 ? 4 : (rem > 0 ? (int)rem : 0);
+  const float* gr = gate + m * K;
+  const float* ur = up + m * K;
+  float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (VEC4 && nvalid == 4) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(gr + k0);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(ur + k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { gv[i] = a[i]; uv[i] = c[i]; }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nvalid) { gv[i] = gr[k0 + i]; uv[i] = ur[k0 + i]; }
+  }
+  float v[4];
+  const bool lane_path = (k0 - kblk) < kv;  // 4-aligned runs never straddle kv
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    v[i] = i < nvalid ? (lane_path ? silu_up_lane(gv[i], uv[i]) : silu_up_tail(gv[i], uv[i]))
+                      : 0.f;
+  uint32_t codes;
+  const float s = quant_block_lane(v, nvalid, &codes);
+  *reinterpret_cast<uint32_t*>(aq + m * Kb * 32 + b * 32 + sub * 4) = codes;
+  if (sub == 0) asc[m * Kb + b] = s;
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+hipError_t launch_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
+                           hipStream_t st) {
+  const int64_t Kb = kb_of(K);
+  const int64_t groups = M * Kb;
+  const dim3 grid((unsigned)((groups + 31) / 32)), block(256);
+  if (K % 4 == 0 && aligned16(A))
+    hipLaunchKernelGGL(quantize_kernel<true>, grid, block, 0, st, M, K, Kb, A, aq, asc);
+  else
+    hipLaunchKernelGGL(quantize_kernel<false>, grid, block, 0, st, M, K, Kb, A, aq, asc);
+  return hipGetLastError();
+}
+
+size_t rmsnorm_quantize_smem(int64_t cols) {
+  return sizeof(float) * (size_t)kRmsRowsPerBlock * (size_t)(cols + 8);
+}
+
+hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
+                                   float eps, int8_t* aq, float* asc, hipStream_t st) {
+  const int64_t Kb = kb_of(cols);
+  const size_t smem = rmsnorm_quantize_smem(cols);
+  const dim3 grid((unsigned)((rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock)),
+      block(64 * kRmsRowsPerBlock);
+  const bool vec4 = cols % 4 == 0 && aligned16(x);
+  hipLaunchKernelGGL(rmsnorm_quantize_kernel, grid, block, smem, st, rows, cols, Kb, x, w, eps,
+                     aq, asc, vec4);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quantize(int64_t M, int64_t K, const float* g, const float* u,
+                                    int8_t* aq, float* asc, hipStream_t st) {
+  const int64_t Kb = kb_of(K);
+  const int64_t groups = M * Kb;
+  const dim3 grid((unsigned)((groups + 31) / 32)), block(256);
+  if (K % 4 == 0 && aligned16(g) && aligned16(u))
+    hipLaunchKernelGGL(silu_mul_quantize_kernel<true>, grid, block, 0, st, M, K, Kb, g, u, aq,
+                       asc);
+  else
+    hipLaunchKernelGGL(silu_mul_quantize_kernel<false>, grid, block, 0, st, M, K, Kb, g, u, aq,
+                       asc);
+  return hipGetLastError();
+}
+
+}  // namespace ovh
