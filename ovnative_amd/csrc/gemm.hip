@@ -5,17 +5,29 @@
 //   f     = fma((float)acc_b, asc[m,b], f)   for b = 0 .. Kb-1 (f starts at +0)
 //   C     = f * wscale[n]             (then C_old + that, rounded separately)
 //
-// Mapping onto the matrix cores: one V_MFMA_I32_32X32X32_I8 consumes exactly one
+// Mapping onto the matrix cores.  One V_MFMA_I32_32X32X32_I8 consumes exactly one
 // 32-k block, so its int32 result IS acc_b for a 32x32 output tile.  Weight rows
 // n are the MFMA's A operand (output rows i) and activation rows m its B operand
-// (output columns j = lane % 32).  A lane then holds 16 accumulators of ONE
-// activation row m, so the block scale asc[m,b] is one register per lane and the
-// per-block epilogue is 16 x (cvt, fma) on values already in registers; wscale
-// is applied once after the K loop.
+// (output columns j = lane % 32): a lane then holds 16 accumulators of ONE
+// activation row, so asc[m,b] is one register per lane and the per-block
+// epilogue is 16 x (cvt, fma) on registers; wscale is applied after the K loop.
+// The epilogue, not the MFMA, bounds this kernel: 32 VALU ops (4 clk each per
+// wavefront) per 32-clk MFMA, so everything else here is arranged to cost no
+// VALU: operands move as 16-byte chunks in MFMA lane order.
 //
-// Tiles: a workgroup computes BN weight rows x BM activation rows with WN x WM
-// wavefronts; K is staged through LDS two blocks (64 bytes) at a time, global
-// loads of the next stage in flight while the current one is multiplied.
+// Layouts.  A "block tile" is 32 rows x 32 k (one MFMA operand, 1 KiB) stored as
+// 64 chunks of 16 bytes in lane order: chunk l = row l%32, k 16*(l/32)..+15.
+//   weights in HBM : [Npad/32][Kb] block tiles (built once at upload), so a
+//                    wavefront loads a block tile as one contiguous 1 KiB;
+//   activations    : row-major int8 [M][Kp] (the quantisers' output), gathered
+//                    into block-tile order on the way to LDS;
+//   LDS            : block tiles in the same order, so fragment reads and
+//                    staging writes are both linear ds_*_b128 (no bank conflicts).
+// K is staged SB blocks at a time through two LDS buffers, one barrier per
+// stage; global loads run two stages ahead (two register sets), because HBM
+// latency on this part is longer than one stage of epilogue work.
+// Workgroups are mapped XCD-aware: the 8 XCDs (blockIdx % 8) each take a
+// contiguous range of weight tiles, so an XCD's L2 holds its own weight slice.
 #include "gemm.h"
 #include "ovh_common.h"
 
@@ -23,31 +35,126 @@ namespace ovh {
 
 namespace {
 
-constexpr int KC = 64;          // K bytes per LDS stage (2 blocks)
-constexpr int LDSS = KC + 16;   // padded LDS row stride (bytes)
+constexpr int TILE = 1024;      // bytes per block tile
 
 __device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b) {
   const i32x16 z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
 
-template <int BN, int BM, int WN, int WM, int MODE>
+// Workgroup id -> (n tile, m tile), XCD-aware.  Workgroups are dispatched to the
+// 8 XCDs round-robin (id % 8).  The n tiles are split into 8 contiguous ranges of
+// `per` tiles (padded: the grid has 8*per*m_tiles workgroups and those landing on
+// a padding tile return at once); XCD x walks its range m-tile by m-tile, so the
+// weight rows an XCD reads stay in its own L2.
+__device__ __forceinline__ bool tile_of(int id, int n_tiles, int& nt, int& mt) {
+  const int per = (n_tiles + 7) >> 3;
+  const int xcd = id & 7, slot = id >> 3;
+  nt = xcd * per + slot % per;
+  mt = slot / per;
+  return nt < n_tiles;
+}
+
+__host__ __device__ inline int64_t grid_size(int64_t n_tiles, int64_t m_tiles) {
+  return 8 * ((n_tiles + 7) / 8) * m_tiles;
+}
+
+// SB = blocks (32 k each) per LDS stage; the host only launches SB with
+// Kb % SB == 0, so the loop below has no K tail and no predicated loads (which
+// would make the compiler drain every outstanding load at each iteration).
+template <int BN, int BM, int WN, int WM, int SB, int MODE>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a) {
-  constexpr int NT = 64 * WN * WM;
+  constexpr int NT = 64 * WN * WM, NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int FN = TN / 32, FM = TM / 32;
   static_assert(FN >= 1 && FM >= 1, "wave tile must hold at least one 32x32 MFMA tile");
-  constexpr int WCH = BN * (KC / 16), ACH = BM * (KC / 16);  // 16-byte chunks per stage
-  constexpr int WPT = (WCH + NT - 1) / NT, APT = (ACH + NT - 1) / NT;
+  constexpr int WT = BN / 32, AT = BM / 32;           // block-tile rows per operand
+  constexpr int LOADS = (WT + AT) * SB;               // block tiles per stage
+  constexpr int LPW = (LOADS + NW - 1) / NW;          // per wavefront
 
-  __shared__ __attribute__((aligned(16))) int8_t sW[BN * LDSS];
-  __shared__ __attribute__((aligned(16))) int8_t sA[BM * LDSS];
-  __shared__ float sS[BM][KC / 32];
+  // Two stage buffers, each [WT weight row tiles | AT activation row tiles] x SB blocks.
+  __shared__ __attribute__((aligned(16))) int8_t smem[2][(WT + AT) * SB * TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WN, wm = wave / WN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int n_tiles = (int)(((int64_t)a.N + BN - 1) / BN);
+  const int m_tiles = (a.M + BM - 1) / BM;
+  int ntile, mtile;
+  if (!tile_of(blockIdx.x, n_tiles, ntile, mtile)) return;  // padding workgroup
+  (void)m_tiles;
+  const int n0 = ntile * BN, m0 = mtile * BM;
+  const int Kb = a.Kb;
   const int64_t Kp = a.Kp;
+  const int nstages = Kb / SB;
+
+  // Per-lane global sources of this wavefront's block-tile loads (LPW of them).
+  // With SB = 4 every wavefront issues the same number of loads; the SB = 1
+  // variants (K % 128 != 0) may leave the last round partial (wave-uniform test).
+  constexpr bool EVEN = LOADS % NW == 0;
+  const int8_t* src[LPW];
+  int lds_off[LPW];  // byte offset inside one stage buffer
+  bool is_w[LPW];
+#pragma unroll
+  for (int t = 0; t < LPW; ++t) {
+    int idx = wave + t * NW;
+    idx = (EVEN || idx < LOADS) ? idx : LOADS - 1;  // surplus slot repeats the last load
+    const int bb = idx % SB, r = idx / SB;  // r < WT: weight row tile, else act row tile
+    is_w[t] = r < WT;
+    if (r < WT) {
+      lds_off[t] = (r * SB + bb) * TILE + lane * 16;
+      src[t] = a.W + ((int64_t)(n0 / 32 + r) * Kb + bb) * TILE + lane * 16;
+    } else {
+      const int rt = r - WT;
+      int row = m0 + rt * 32 + (lane & 31);
+      row = row < a.M ? row : a.M - 1;  // rows are independent: clamp, discard later
+      lds_off[t] = WT * SB * TILE + (rt * SB + bb) * TILE + lane * 16;
+      src[t] = a.aq + (int64_t)row * Kp + bb * 32 + (lane >> 5) * 16;
+    }
+  }
+
+  // Scale rows of this lane's m tiles.
+  const float* srow[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    int row = m0 + wm * TM + j * 32 + (lane & 31);
+    row = row < a.M ? row : a.M - 1;
+    srow[j] = (MODE == kDumpBlocks) ? nullptr : a.asc + (int64_t)row * Kb;
+  }
+
+  // Two register sets of prefetched stages (even / odd): the loads for stage
+  // s+2 are issued right after stage s lands in LDS, so two stages of compute
+  // cover each load's latency.  Prefetches past the end re-read the last stage
+  // (harmless) so that every iteration issues the same loads unconditionally.
+  i32x4 regs0[LPW], regs1[LPW];
+  float scr0[FM][SB], scr1[FM][SB];
+
+  auto load_stage = [&](int s, i32x4 (&regs)[LPW], float (&scn)[FM][SB])
+                        __attribute__((always_inline)) {
+    s = s < nstages ? s : nstages - 1;
+    const int kb0 = s * SB;
+#pragma unroll
+    for (int t = 0; t < LPW; ++t) {
+      const int64_t step = is_w[t] ? (int64_t)kb0 * TILE : (int64_t)kb0 * 32;
+      regs[t] = *reinterpret_cast<const i32x4*>(src[t] + step);
+    }
+    if (MODE != kDumpBlocks) {
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        if constexpr (SB == 4) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(srow[j] + kb0);
+#pragma unroll
+          for (int bb = 0; bb < SB; ++bb) scn[j][bb] = v[bb];
+        } else {
+#pragma unroll
+          for (int bb = 0; bb < SB; ++bb) scn[j][bb] = srow[j][kb0 + bb];
+        }
+      }
+    }
+  };
+  auto store_stage = [&](int8_t* base, const i32x4 (&regs)[LPW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < LPW; ++t) *reinterpret_cast<i32x4*>(base + lds_off[t]) = regs[t];
+  };
 
   f32x16 f[FN][FM];
 #pragma unroll
@@ -57,95 +164,88 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[i][j][e] = 0.f;
 
-  i32x4 wreg[WPT], areg[APT];
-  float sreg = 0.f;
-
-  auto gload = [&](int64_t kc) {
+  float sc[FM][SB];
+  auto read_frags = [&](const int8_t* base, int bb, i32x4 (&af)[FN], i32x4 (&bf)[FM])
+                        __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < WPT; ++t) {
-      const int c = tid + t * NT;
-      const int r = c / (KC / 16), col = c % (KC / 16);
-      const int64_t k = kc + col * 16;
-      i32x4 v = {0, 0, 0, 0};
-      if (c < WCH && k < Kp) v = *reinterpret_cast<const i32x4*>(a.W + (int64_t)(n0 + r) * Kp + k);
-      wreg[t] = v;
-    }
+    for (int i = 0; i < FN; ++i)
+      af[i] = *reinterpret_cast<const i32x4*>(base + ((wn * FN + i) * SB + bb) * TILE + lane * 16);
 #pragma unroll
-    for (int t = 0; t < APT; ++t) {
-      const int c = tid + t * NT;
-      const int r = c / (KC / 16), col = c % (KC / 16);
-      const int64_t k = kc + col * 16;
-      i32x4 v = {0, 0, 0, 0};
-      if (c < ACH && k < Kp && m0 + r < a.M)
-        v = *reinterpret_cast<const i32x4*>(a.aq + (int64_t)(m0 + r) * Kp + k);
-      areg[t] = v;
-    }
-    if (MODE != kDumpBlocks && tid < BM * (KC / 32)) {
-      const int r = tid / (KC / 32), bb = tid % (KC / 32);
-      const int64_t b = kc / 32 + bb;
-      sreg = (m0 + r < a.M && b < a.Kb) ? a.asc[(int64_t)(m0 + r) * a.Kb + b] : 0.f;
-    }
+    for (int j = 0; j < FM; ++j)
+      bf[j] = *reinterpret_cast<const i32x4*>(base + WT * SB * TILE +
+                                              ((wm * FM + j) * SB + bb) * TILE + lane * 16);
   };
-  auto sstore = [&]() {
+  auto mfmas = [&](const i32x4 (&af)[FN], const i32x4 (&bf)[FM], i32x16 (&acc)[FN][FM])
+                   __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < WPT; ++t) {
-      const int c = tid + t * NT;
-      if (c < WCH) {
-        const int r = c / (KC / 16), col = c % (KC / 16);
-        *reinterpret_cast<i32x4*>(sW + r * LDSS + col * 16) = wreg[t];
-      }
-    }
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int t = 0; t < APT; ++t) {
-      const int c = tid + t * NT;
-      if (c < ACH) {
-        const int r = c / (KC / 16), col = c % (KC / 16);
-        *reinterpret_cast<i32x4*>(sA + r * LDSS + col * 16) = areg[t];
-      }
-    }
-    if (tid < BM * (KC / 32)) sS[tid / (KC / 32)][tid % (KC / 32)] = sreg;
+      for (int j = 0; j < FM; ++j) acc[i][j] = mfma_i8(af[i], bf[j]);
   };
-
-  gload(0);
-  for (int64_t kc = 0; kc < Kp; kc += KC) {
-    __syncthreads();  // previous stage fully consumed
-    sstore();
-    __syncthreads();
-    if (kc + KC < Kp) gload(kc + KC);  // next stage's loads overlap this stage's math
-    const int nblk = (Kp - kc) >= KC ? 2 : 1;
-    for (int bb = 0; bb < nblk; ++bb) {
-      i32x4 af[FN], bf[FM];
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-        af[i] = *reinterpret_cast<const i32x4*>(sW + (wn * TN + i * 32 + (lane & 31)) * LDSS +
-                                                bb * 32 + (lane >> 5) * 16);
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        bf[j] = *reinterpret_cast<const i32x4*>(sA + (wm * TM + j * 32 + (lane & 31)) * LDSS +
-                                                bb * 32 + (lane >> 5) * 16);
+  auto epilogue = [&](const i32x16 (&acc)[FN][FM], int s, int bb) __attribute__((always_inline)) {
+    if (MODE == kDumpBlocks) {
+      const int64_t b = (int64_t)s * SB + bb;
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        const float s = sS[wm * TM + j * 32 + (lane & 31)][bb];
+        const int m = m0 + wm * TM + j * 32 + (lane & 31);
+        if (m >= a.M) continue;
 #pragma unroll
-        for (int i = 0; i < FN; ++i) {
-          const i32x16 acc = mfma_i8(af[i], bf[j]);
-          if (MODE == kDumpBlocks) {
-            const int m = m0 + wm * TM + j * 32 + (lane & 31);
-            const int64_t b = kc / 32 + bb;
-            if (m < a.M) {
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-              for (int e = 0; e < 16; ++e) {
-                const int n = n0 + wn * TN + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (n < a.N) a.dump[((int64_t)m * a.N + n) * a.Kb + b] = acc[e];
-              }
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) f[i][j][e] = fmaf((float)acc[e], s, f[i][j][e]);
+          for (int e = 0; e < 16; ++e) {
+            const int n = n0 + wn * TN + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (n < a.N) a.dump[((int64_t)m * a.N + n) * Kb + b] = acc[i][j][e];
           }
-        }
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            f[i][j][e] = fmaf((float)acc[i][j][e], sc[j][bb], f[i][j][e]);
     }
+  };
+  // Software pipeline over the SB blocks of a stage: fragments are read two
+  // blocks ahead and the MFMAs of block bb+1 are issued before the epilogue of
+  // block bb, so the matrix core, the LDS reads and the VALU epilogue overlap
+  // within one wavefront (two fragment and two accumulator register sets).
+  auto compute_stage = [&](const int8_t* base, int s) __attribute__((always_inline)) {
+    i32x4 af[2][FN], bf[2][FM];
+    i32x16 acc[2][FN][FM];
+    read_frags(base, 0, af[0], bf[0]);
+    if (SB > 1) read_frags(base, 1, af[1], bf[1]);
+    mfmas(af[0], bf[0], acc[0]);
+#pragma unroll
+    for (int bb = 0; bb < SB; ++bb) {
+      const int cur = bb & 1, nxt = cur ^ 1;
+      if (bb + 1 < SB) mfmas(af[nxt], bf[nxt], acc[nxt]);
+      if (bb + 2 < SB) read_frags(base, bb + 2, af[cur], bf[cur]);
+      epilogue(acc[cur], s, bb);
+    }
+  };
+  auto take_scales = [&](const float (&scn)[FM][SB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int bb = 0; bb < SB; ++bb) sc[j][bb] = scn[j][bb];
+  };
+
+  load_stage(0, regs0, scr0);
+  load_stage(1, regs1, scr1);
+  for (int s = 0; s < nstages; s += 2) {
+    store_stage(smem[0], regs0);
+    take_scales(scr0);
+    __syncthreads();
+    load_stage(s + 2, regs0, scr0);
+    compute_stage(smem[0], s);
+    if (s + 1 >= nstages) break;
+    store_stage(smem[1], regs1);
+    take_scales(scr1);
+    __syncthreads();
+    load_stage(s + 3, regs1, scr1);
+    compute_stage(smem[1], s + 1);
   }
   if (MODE == kDumpBlocks) return;
 
@@ -192,49 +292,70 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
   }
 }
 
-template <int BN, int BM, int WN, int WM>
-hipError_t launch_cfg(const GemmArgs& a, GemmMode mode, hipStream_t st, int64_t Npad) {
-  const dim3 grid((unsigned)(Npad / BN), (unsigned)((a.M + BM - 1) / BM)), block(64 * WN * WM);
+template <int BN, int BM, int WN, int WM, int SB>
+hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
+  const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
   switch (mode) {
     case kStore:
-      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, kStore>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, SB, kStore>), grid, block, 0, st, a);
       break;
     case kAccumulate:
-      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, kAccumulate>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, SB, kAccumulate>), grid, block, 0, st, a);
       break;
     case kDumpBlocks:
-      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, kDumpBlocks>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, SB, kDumpBlocks>), grid, block, 0, st, a);
       break;
   }
   return hipGetLastError();
 }
 
+// Stages of 4 blocks when K allows it (every LM projection: K = 1024/2048/3072),
+// single-block stages otherwise.
+template <int BN, int BM, int WN, int WM>
+hipError_t launch_cfg(const GemmArgs& a, GemmMode mode, hipStream_t st) {
+  if (a.Kb % 4 == 0) return launch_cfg_sb<BN, BM, WN, WM, 4>(a, mode, st);
+  return launch_cfg_sb<BN, BM, WN, WM, 1>(a, mode, st);
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
-  const int64_t Npad = ((int64_t)a.N + kRowPad - 1) / kRowPad * kRowPad;
-  // Largest tile that still gives every CU a workgroup; the smallest otherwise.
-  auto tiles = [&](int bn, int bm) { return (Npad / bn) * (((int64_t)a.M + bm - 1) / bm); };
-  constexpr int64_t kCUs = 256;
-  if (a.M > 64 && tiles(128, 128) >= kCUs) return launch_cfg<128, 128, 2, 2>(a, mode, st, Npad);
-  if (a.M > 32 && tiles(128, 64) >= kCUs) return launch_cfg<128, 64, 2, 2>(a, mode, st, Npad);
-  if (a.M > 32 && tiles(64, 64) >= kCUs) return launch_cfg<64, 64, 2, 2>(a, mode, st, Npad);
-  if (tiles(64, 32) >= kCUs) return launch_cfg<64, 32, 2, 1>(a, mode, st, Npad);
-  return launch_cfg<32, 32, 1, 1>(a, mode, st, Npad);
+  // Tile choice, from a sweep of every config on MI355X over the LM shapes
+  // (M = 128 / 600 / 16384, N = 1024..8192, K = 1024..3072): wide-N shapes at
+  // M >= 512 keep a 128x64 tile (wave 64x32: one weight fragment feeds two
+  // MFMAs), mid-size ones 64x64, and skinny M or N = 1024 one-wave 32x32 tiles,
+  // which give the most wavefronts for the few output tiles there are.
+  const int64_t M = a.M, N = a.N;
+  if (M >= 2048 || (M >= 512 && N >= 6144)) return launch_cfg<128, 64, 2, 2>(a, mode, st);
+  if (M >= 256) return launch_cfg<64, 64, 2, 2>(a, mode, st);
+  return launch_cfg<32, 32, 1, 1>(a, mode, st);
 }
 
 // ---------------------------------------------------------------------------
-// Weight layout: OVW1 int8 in layout 0 ([N,K]) or 1 ([K,N]) -> [Npad][Kp] with
-// zero padding; scales -> [Npad] with zeros.  Load-time only.
-__global__ void weight_layout_kernel(int64_t N, int64_t K, int64_t Npad, int64_t Kp,
+// Weight layout: OVW1 int8 in layout 0 ([N,K]) or 1 ([K,N]) -> block tiles
+// [Npad/32][Kb][64 lanes][16 bytes] with zero padding (rows >= N, k >= K);
+// scales -> [Npad] with zeros.  Load-time only: one thread per 16-byte chunk.
+__global__ void weight_layout_kernel(int64_t N, int64_t K, int64_t Npad, int64_t Kb,
                                      const int8_t* __restrict__ src, int layout,
                                      int8_t* __restrict__ dst) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= Npad * Kp) return;
-  const int64_t n = idx / Kp, k = idx - n * Kp;
-  int8_t v = 0;
-  if (n < N && k < K) v = layout == 0 ? src[n * K + k] : src[k * N + n];
-  dst[idx] = v;
+  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = Npad / 32 * Kb * 64;
+  if (chunk >= total) return;
+  const int lane = (int)(chunk & 63);
+  const int64_t tile = chunk >> 6;
+  const int64_t rt = tile / Kb, b = tile - rt * Kb;
+  const int64_t n = rt * 32 + (lane & 31);
+  const int64_t k0 = b * 32 + (lane >> 5) * 16;
+  int8_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t k = k0 + i;
+    v[i] = (n < N && k < K) ? (layout == 0 ? src[n * K + k] : src[k * N + n]) : (int8_t)0;
+  }
+  int8_t* o = dst + chunk * 16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = v[i];
 }
 
 __global__ void scale_pad_kernel(int64_t N, int64_t Npad, const float* __restrict__ src,
@@ -243,19 +364,21 @@ __global__ void scale_pad_kernel(int64_t N, int64_t Npad, const float* __restric
   if (i < Npad) dst[i] = i < N ? src[i] : 0.f;
 }
 
-__global__ void weight_to_nk_kernel(int64_t N, int64_t K, int64_t Kp,
+__global__ void weight_to_nk_kernel(int64_t N, int64_t K, int64_t Kb,
                                     const int8_t* __restrict__ src, int8_t* __restrict__ dst) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= N * K) return;
   const int64_t n = idx / K, k = idx - n * K;
-  dst[idx] = src[n * Kp + k];
+  const int64_t rt = n / 32, b = k / 32;
+  const int lane = (int)(n % 32) + 32 * (int)((k % 32) / 16);
+  dst[idx] = src[((rt * Kb + b) * 64 + lane) * 16 + (k % 16)];
 }
 
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
                                 const float* scale_src, DeviceWeight& w, hipStream_t st) {
-  const int64_t total = w.Npad * w.Kp;
-  hipLaunchKernelGGL(weight_layout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     st, N, K, w.Npad, w.Kp, src, layout, w.q);
+  const int64_t chunks = w.Npad / 32 * w.Kb * 64;
+  hipLaunchKernelGGL(weight_layout_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     st, N, K, w.Npad, w.Kb, src, layout, w.q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(scale_pad_kernel, dim3((unsigned)((w.Npad + 255) / 256)), dim3(256), 0, st,
@@ -266,7 +389,7 @@ hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int lay
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st) {
   const int64_t total = w.N * w.K;
   hipLaunchKernelGGL(weight_to_nk_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                     w.N, w.K, w.Kp, w.q, q_nk);
+                     w.N, w.K, w.Kb, w.q, q_nk);
   return hipGetLastError();
 }
 

@@ -1,0 +1,23 @@
+// Tuning harness: every tile config of gemm.hip callable by index, for the tile
+// sweep (tune_gemm.py) and single-shape profiling runs (one_gemm.py).  Not part
+// of libovnative_amd.so.
+#include "../csrc/gemm.hip"
+using namespace ovh;
+extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
+                         const int8_t* W, const float* ws, float* C, int accumulate, void* st) {
+  GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
+  a.W = W; a.ws = ws; a.nslices = 1; a.start[0] = 0; a.start[1] = N; a.out[0] = C; a.ld[0] = N;
+  GemmMode mode = accumulate ? kAccumulate : kStore;
+  hipStream_t s = (hipStream_t)st;
+  switch (cfg) {
+    case 0: return launch_cfg<128, 128, 2, 2>(a, mode, s);
+    case 1: return launch_cfg<64, 128, 2, 2>(a, mode, s);
+    case 2: return launch_cfg<64, 64, 2, 2>(a, mode, s);
+    case 3: return launch_cfg<32, 64, 1, 2>(a, mode, s);
+    case 4: return launch_cfg<128, 64, 2, 2>(a, mode, s);
+    case 5: return launch_cfg<32, 128, 1, 4>(a, mode, s);
+    case 6: return launch_cfg<64, 32, 2, 1>(a, mode, s);
+    case 7: return launch_cfg<32, 32, 1, 1>(a, mode, s);
+  }
+  return -1;
+}

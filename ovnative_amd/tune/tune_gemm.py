@@ -1,0 +1,44 @@
+"""Sweep every GEMM tile config over the LM shapes; checks each against the
+product kernel bit for bit and prints per-config time.
+
+    python3 ovnative_amd/tune/tune_gemm.py
+"""
+import ctypes as C, sys, os
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+import torch, ovnative_amd as ov
+torch.cuda.set_device(0)
+lib = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libgemm_tune.so'))
+lib.tune_gemm.argtypes = [C.c_int]*4 + [C.c_void_p]*5 + [C.c_int, C.c_void_p]
+class DW(C.Structure):
+    _fields_ = [('N', C.c_int64), ('K', C.c_int64), ('Npad', C.c_int64), ('Kb', C.c_int64), ('Kp', C.c_int64), ('q', C.c_void_p), ('scale', C.c_void_p)]
+cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x128', 6: '64x32', 7: '32x32'}
+shapes = [(600, 6144, 1024), (600, 4096, 1024), (600, 1024, 2048), (600, 1024, 3072), (600, 8192, 1024),
+          (128, 4096, 1024), (128, 6144, 1024), (128, 1024, 2048), (128, 1024, 3072), (128, 2048, 1024), (128, 1024, 1024),
+          (256, 3072, 1024), (16384, 6144, 1024), (16384, 1024, 3072)]
+st = torch.cuda.current_stream()
+for (M, N, K) in shapes:
+    q = torch.randint(-127, 128, (N, K), dtype=torch.int8, device='cuda')
+    s = torch.rand(N, device='cuda') * 1e-3 + 1e-4
+    w = ov.Weight.from_device(q, s)
+    dw = DW.from_address(w.handle.value)
+    A = torch.randn(M, K, device='cuda')
+    aq, asc = ov.s8_nk_quantize(A)
+    ref = ov.linear_q(aq, asc, w)
+    res = []
+    for cfg, name in cfgs.items():
+        C_ = torch.empty(M, N, device='cuda')
+        args = (cfg, M, N, K // 32, aq.data_ptr(), asc.data_ptr(), dw.q, dw.scale, C_.data_ptr(), 0, st.cuda_stream)
+        rc = lib.tune_gemm(*args); torch.cuda.synchronize()
+        ok = torch.equal(C_.view(torch.int32), ref.view(torch.int32))
+        n = 30 if M * N * K < 1e11 else 8
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(3): lib.tune_gemm(*args)
+        e0.record()
+        for _ in range(n): lib.tune_gemm(*args)
+        e1.record(); torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / n * 1e3
+        res.append((us, name, ok))
+    res.sort()
+    print(f"M={M} N={N} K={K}: " + "  ".join(f"{nm}:{us:.1f}us{'' if ok else '!BAD'}" for us, nm, ok in res)
+          + f"  | best {2*M*N*K/res[0][0]/1e6:.0f} TOPS", flush=True)

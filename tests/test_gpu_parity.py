@@ -170,7 +170,7 @@ def _oracle_linear(oracle, A, q, s, Cin=None):
     (256, 3072, 1024),
     (128, 2048, 1024), (128, 1024, 1024), (128, 1024, 2048), (128, 3072, 1024),
     (128, 1024, 3072),   # config 2: q, k/v, o, gate/up, down at M = 2 x 64
-    (600, 4096, 1024), (600, 1024, 3072),  # config 3/4 shapes (merged qkv, down)
+    (600, 4096, 1024), (600, 6144, 1024), (600, 1024, 3072),  # config 3/4: qkv, gate/up, down
     (1, 1024, 1024), (5, 200, 96), (33, 130, 1000), (65, 64, 32),
 ])
 def test_linear_vs_oracle(oracle, M, N, K):
