@@ -135,6 +135,42 @@ int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t 
  * bit-exactness check. */
 int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream);
 
+/* ---- attention side of a decoder layer (fp32) ------------------------------- */
+
+/* One attention segment: `rows` query rows starting at element offset q_off of
+ * q and out, attending to the `rows` keys at element offset kv_off of k and v,
+ * with an optional additive bias [rows, rows] (device; NULL = none).  Same
+ * fields and meaning as ov::AttnSegment (cpp/src/model/lm.h:42-51). */
+typedef struct OvhAttnSegment {
+  const float* bias;
+  int32_t rows;
+  int64_t q_off;
+  int64_t kv_off;
+} OvhAttnSegment;
+
+/* RoPE cos/sin tables [rows, head_dim/2] from device int64 positions, as
+ * qk_norm_rope_f32 builds them (ops_cpu.cpp:958-993): inv_freq = (float)
+ * pow(theta, -2i/D) in double, angle = (float)pos * inv_freq.  cos/sin are
+ * correctly rounded (libm's cosf/sinf are within one ulp of them). */
+int ovh_rope_tables(int64_t rows, const int64_t* pos, int head_dim, float theta, float* cos_tab,
+                    float* sin_tab, void* stream);
+/* qk_norm_rope_f32 (ops.h, ops_cpu.cpp:945-1016 -> :266-318): per-head RMSNorm
+ * (weights qw / kw [head_dim]) then RoPE, in place on q [rows, n_heads*D] and
+ * k [rows, n_kv_heads*D], with the tables of ovh_rope_tables.  Bit-identical
+ * to the reference for the same tables.  head_dim 64 or 128. */
+int ovh_qk_norm_rope(float* q, float* k, const float* qw, const float* kw, int64_t rows,
+                     int n_heads, int n_kv_heads, int head_dim, const float* cos_tab,
+                     const float* sin_tab, float eps, void* stream);
+/* The attention loop of LM::run_layer (lm.cpp:259-276) over attention_head_f32
+ * (ops.h, ops_cpu.cpp:907-943): for each segment and query head h (KV head
+ * h / (n_heads / n_kv_heads)), out = softmax(q k^T * scale + bias) v in fp32,
+ * zeros for a fully masked row (max < -1e29).  q/out rows have stride q_stride
+ * / out_stride, k/v rows kv_stride (elements).  head_dim 128.  segs is HOST
+ * memory (any count; launched 32 segments at a time). */
+int ovh_attention(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_heads,
+                  int head_dim, const float* q, int64_t q_stride, const float* k, const float* v,
+                  int64_t kv_stride, float scale, float* out, int64_t out_stride, void* stream);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

@@ -75,6 +75,15 @@ class Oracle:
             "ovo_linear_q_packed": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64,
                                               C.c_int]),
             "ovo_num_threads": (C.c_int, []),
+            "ovo_rope_tables": (None, [_i64, _p, C.c_int, _f32, _p, _p]),
+            "ovo_qk_norm_rope": (C.c_int, [_p, _p, _p, _p, _i64, C.c_int, C.c_int, C.c_int, _p,
+                                           _p, _f32]),
+            "ovo_attention_head": (C.c_int, [_p, _i64, _p, _p, _i64, _p, C.c_int, C.c_int, _f32,
+                                             _p, _i64]),
+            "ovo_attention": (C.c_int, [C.c_int, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, _p,
+                                        _p, _p, _f32, _p]),
+            "ovo_embed": (C.c_int, [C.c_int, C.c_int, C.c_int, _i64, _p, _p, _p, _p, _p, _i64, _p,
+                                    _p, _p, _i64, _p, _p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -185,6 +194,88 @@ class Oracle:
     def num_threads(self) -> int:
         return int(self.lib.ovo_num_threads())
 
+    # -- the rest of the layer ----------------------------------------------
+    def rope_tables(self, pos: np.ndarray, D: int, theta: float = 1e6):
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        c = np.empty((pos.size, D // 2), np.float32)
+        s = np.empty((pos.size, D // 2), np.float32)
+        self.lib.ovo_rope_tables(pos.size, _ptr(pos), D, theta, _ptr(c), _ptr(s))
+        return c, s
+
+    def qk_norm_rope(self, q, k, qw, kw, n_heads, n_kv_heads, D, pos=None, theta=1e6,
+                     eps=1e-6, tables=None):
+        """Returns new (q, k); q [rows, n_heads*D], k [rows, n_kv_heads*D]."""
+        q = np.array(q, dtype=np.float32, copy=True, order="C")
+        k = np.array(k, dtype=np.float32, copy=True, order="C")
+        qw = np.ascontiguousarray(qw, dtype=np.float32)
+        kw = np.ascontiguousarray(kw, dtype=np.float32)
+        c, s = tables if tables is not None else self.rope_tables(pos, D, theta)
+        c = np.ascontiguousarray(c, dtype=np.float32)
+        s = np.ascontiguousarray(s, dtype=np.float32)
+        rc = self.lib.ovo_qk_norm_rope(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw), q.shape[0],
+                                       n_heads, n_kv_heads, D, _ptr(c), _ptr(s), eps)
+        if rc != 0:
+            raise ValueError("qk_norm_rope: head_dim/2 must be a multiple of 8")
+        return q, k
+
+    def attention_head(self, q, k, v, bias=None, scale=None):
+        """q, k, v [S, D] (one head), bias [S, S] or None."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        S, D = q.shape
+        scale = np.float32(1.0) / np.sqrt(np.float32(D)) if scale is None else scale
+        out = np.empty((S, D), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        rc = self.lib.ovo_attention_head(_ptr(q), D, _ptr(k), _ptr(v), D,
+                                         None if b is None else _ptr(b), S, D, float(scale),
+                                         _ptr(out), D)
+        if rc != 0:
+            raise ValueError("attention_head: head_dim must be a multiple of 8")
+        return out
+
+    def attention(self, q, k, v, segs, n_heads, n_kv_heads, D, scale=None):
+        """GQA over segments: segs = [(bias or None, rows, q_row0, kv_row0)] with row
+        offsets into q [T, n_heads*D] and k/v [T, n_kv_heads*D]."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(D)) if scale is None else scale
+        out = np.zeros_like(q)
+        n = len(segs)
+        keep = [None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+                for b, *_ in segs]
+        bias = (C.c_void_p * n)(*[None if b is None else b.ctypes.data for b in keep])
+        rows = np.array([r for _, r, _, _ in segs], np.int32)
+        qo = np.array([qr * n_heads * D for _, _, qr, _ in segs], np.int64)
+        ko = np.array([kr * n_kv_heads * D for _, _, _, kr in segs], np.int64)
+        rc = self.lib.ovo_attention(n, C.cast(bias, C.c_void_p), _ptr(rows), _ptr(qo), _ptr(ko),
+                                    n_heads, n_kv_heads, D, _ptr(q), _ptr(k), _ptr(v),
+                                    float(scale), _ptr(out))
+        if rc != 0:
+            raise ValueError("attention: bad head configuration")
+        return out
+
+    def embed(self, ids, mask, tok, aud, offsets, tok_scale=None, aud_scale=None):
+        """ids [B, C, S] int64, mask [B, S] u8; tables fp32, or int8 with per-row scales."""
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        mask = np.ascontiguousarray(mask, dtype=np.uint8)
+        offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+        B, Cb, S = ids.shape
+        H = tok.shape[1]
+        out = np.empty((B * S, H), np.float32)
+        tf = tok if tok.dtype == np.float32 else None
+        af = aud if aud.dtype == np.float32 else None
+        tq = None if tf is not None else np.ascontiguousarray(tok, dtype=np.int8)
+        aqq = None if af is not None else np.ascontiguousarray(aud, dtype=np.int8)
+        ptr = lambda a: None if a is None else _ptr(np.ascontiguousarray(a))
+        rc = self.lib.ovo_embed(B, S, Cb, H, _ptr(ids), _ptr(mask), ptr(tf), ptr(tq),
+                                ptr(tok_scale), tok.shape[0], ptr(af), ptr(aqq), ptr(aud_scale),
+                                aud.shape[0], _ptr(offsets), _ptr(out))
+        if rc != 0:
+            raise ValueError("embed: id out of range")
+        return out
+
 
 class Reference:
     """The reference's compiled CPU kernels (see ``oracle/ref_shim.cpp``)."""
@@ -222,6 +313,29 @@ class Reference:
 
     def vnni_available(self) -> bool:
         return bool(self.lib.ovref_vnni_available())
+
+    def qk_norm_rope(self, q, k, qw, kw, n_heads, n_kv_heads, D, pos, theta=1e6, eps=1e-6):
+        q = np.array(q, dtype=np.float32, copy=True, order="C")
+        k = np.array(k, dtype=np.float32, copy=True, order="C")
+        qw = np.ascontiguousarray(qw, dtype=np.float32)
+        kw = np.ascontiguousarray(kw, dtype=np.float32)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        self.lib.ovref_qk_norm_rope(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw), q.shape[0], n_heads,
+                                    n_kv_heads, D, _ptr(pos), theta, eps)
+        return q, k
+
+    def attention_head(self, q, k, v, bias=None, scale=None):
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        S, D = q.shape
+        scale = np.float32(1.0) / np.sqrt(np.float32(D)) if scale is None else scale
+        out = np.empty((S, D), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self.lib.ovref_attention_head(_ptr(q), D, _ptr(k), _ptr(v), D,
+                                      None if b is None else _ptr(b), S, D, float(scale),
+                                      _ptr(out), D)
+        return out
 
     def kernel_name(self) -> str:
         return self.lib.ovref_kernel_name().decode()

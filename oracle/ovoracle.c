@@ -60,7 +60,10 @@
  * golden vectors catch it (never set in a normal build):
  *   1 unfused exp256 range reduction   2 sequential RMSNorm sum
  *   3 unfused block epilogue           4 truncating quantiser
- *   5 wrong zero point (127)           6 weight scale floor skipped */
+ *   5 wrong zero point (127)           6 weight scale floor skipped
+ *   7 attention scale applied after the lane sum
+ *   8 RoPE rotation with both products rounded (no fma)
+ *   9 softmax through libm expf everywhere (no exp256) */
 #ifndef OVO_PLANT
 #define OVO_PLANT 0
 #endif
@@ -452,4 +455,231 @@ OVO_API int ovo_num_threads(void) {
 #else
   return 1;
 #endif
+}
+
+/* ========================================================================
+ * The rest of one decoder layer and the LM around the linears.
+ *
+ *   ovo_rope_tables     cpp/src/backend/cpu/ops_cpu.cpp:945-993 (qk_norm_rope_f32
+ *                       table build: inv_freq in double, angle and cos/sin in float)
+ *   ovo_qk_norm_rope    cpp/src/backend/cpu/ops_cpu.cpp:266-299, 301-318
+ *                       (norm_rope_head_avx2 / qk_norm_rope_avx2, half % 8 == 0)
+ *   ovo_attention_head  cpp/src/backend/cpu/ops_cpu.cpp:586-786
+ *                       (attention_head_avx2_rb4; rb2 at :332-578 has the same
+ *                       per-row arithmetic), run under FTZ/DAZ like the reference
+ *   ovo_attention       cpp/src/model/lm.cpp:259-276 (GQA loop over segments/heads)
+ *   ovo_embed           cpp/src/model/lm.cpp:180-198, mat.cpp:57-67 (Emb::gather)
+ * ====================================================================== */
+
+/* FTZ/DAZ as enable_flush_to_zero() sets them (ops_cpu.cpp:1132-1136). */
+static inline unsigned ftz_enter(void) {
+#if defined(__x86_64__)
+  const unsigned old = _mm_getcsr();
+  _mm_setcsr(old | 0x8040u);
+  return old;
+#else
+  return 0;
+#endif
+}
+static inline void ftz_leave(unsigned old) {
+#if defined(__x86_64__)
+  _mm_setcsr(old);
+#else
+  (void)old;
+#endif
+}
+
+/* cos/sin tables [rows, D/2]: inv_freq[i] = (float)pow(theta, -2i/D) in double,
+ * angle = (float)pos * inv_freq[i] in float, then cosf/sinf. */
+OVO_API void ovo_rope_tables(int64_t rows, const int64_t* pos, int D, float theta,
+                             float* cos_tab, float* sin_tab) {
+  const int half = D / 2;
+  float inv_freq[512];
+  if (half > 512) return;
+  for (int i = 0; i < half; ++i)
+    inv_freq[i] = (float)pow((double)theta, -2.0 * i / (double)D);
+  for (int64_t r = 0; r < rows; ++r) {
+    const float p = (float)pos[r];
+    for (int i = 0; i < half; ++i) {
+      const float angle = p * inv_freq[i];
+      cos_tab[r * half + i] = cosf(angle);
+      sin_tab[r * half + i] = sinf(angle);
+    }
+  }
+}
+
+/* The row's sum of squares in the order of an 8-lane fma accumulator: lane j
+ * takes elements j, j+8, ...; lanes summed left to right.  D % 8 == 0. */
+static inline float lanes8_sumsq(const float* v, int D) {
+  float lanes[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i + 8 <= D; i += 8)
+    for (int j = 0; j < 8; ++j) lanes[j] = fmaf(v[i + j], v[i + j], lanes[j]);
+  float sum = lanes[0];
+  for (int j = 1; j < 8; ++j) sum = sum + lanes[j];
+  return sum;
+}
+
+static void norm_rope_head(float* v, const float* w, const float* c, const float* sn, int D,
+                           float eps) {
+  const int half = D / 2;
+  const float sum = lanes8_sumsq(v, D);
+  const float scale = 1.f / sqrtf(sum / (float)D + eps);
+  for (int i = 0; i < half; ++i) {
+    const float na = (v[i] * scale) * w[i];
+    const float nb = (v[i + half] * scale) * w[i + half];
+    /* _mm256_fmsub_ps(na, c, nb*sn) and _mm256_fmadd_ps(na, sn, nb*c) */
+    if (OVO_PLANT == 8) {
+      v[i] = na * c[i] - nb * sn[i];
+      v[i + half] = na * sn[i] + nb * c[i];
+      continue;
+    }
+    v[i] = fmaf(na, c[i], -(nb * sn[i]));
+    v[i + half] = fmaf(na, sn[i], nb * c[i]);
+  }
+}
+
+/* q [rows, n_heads*D], k [rows, n_kv_heads*D] in place.  Returns -1 when
+ * D/2 % 8 != 0 (the reference then takes its scalar fallback, not restated). */
+OVO_API int ovo_qk_norm_rope(float* q, float* k, const float* qw, const float* kw, int64_t rows,
+                             int n_heads, int n_kv_heads, int D, const float* cos_tab,
+                             const float* sin_tab, float eps) {
+  if (D <= 0 || (D / 2) % 8 != 0) return -1;
+  const int half = D / 2;
+#pragma omp parallel for schedule(static) if (rows >= 16)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* c = cos_tab + r * half;
+    const float* sn = sin_tab + r * half;
+    for (int h = 0; h < n_heads; ++h)
+      norm_rope_head(q + (r * n_heads + h) * D, qw, c, sn, D, eps);
+    for (int h = 0; h < n_kv_heads; ++h)
+      norm_rope_head(k + (r * n_kv_heads + h) * D, kw, c, sn, D, eps);
+  }
+  return 0;
+}
+
+/* hsum256: ((v0+v4) + (v1+v5)) + ((v2+v6) + (v3+v7)). */
+static inline float hsum8(const float* v) {
+  const float l0 = v[0] + v[4], l1 = v[1] + v[5], l2 = v[2] + v[6], l3 = v[3] + v[7];
+  return (l0 + l1) + (l2 + l3);
+}
+
+/* One head, S queries attending to S keys (fp32, additive bias [S, S] or NULL).
+ * Scores: 8 fma lanes over d, each lane times scale, hsum8, plus bias.  A row
+ * whose max is below -1e29 is fully masked and gets zeros.  Softmax: exp256 on
+ * the first S/8*8 keys (lane sums, hsum8), libm expf on the tail, one 1/sum
+ * multiply.  Output: sequential fma over keys.  D % 8 == 0. */
+OVO_API int ovo_attention_head(const float* q, int64_t q_stride, const float* k, const float* v,
+                               int64_t kv_stride, const float* bias, int S, int D, float scale,
+                               float* out, int64_t out_stride) {
+  if (S <= 0) return 0;
+  if (D <= 0 || D % 8 != 0) return -1;
+  const unsigned csr = ftz_enter();
+  float* p = (float*)malloc(sizeof(float) * (size_t)S);
+  if (!p) { ftz_leave(csr); return -1; }
+  for (int s = 0; s < S; ++s) {
+    const float* qr = q + (int64_t)s * q_stride;
+    const float* br = bias ? bias + (int64_t)s * S : NULL;
+    float mx = -INFINITY;
+    for (int t = 0; t < S; ++t) {
+      const float* kr = k + (int64_t)t * kv_stride;
+      float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int d = 0; d + 8 <= D; d += 8)
+        for (int j = 0; j < 8; ++j) a[j] = fmaf(qr[d + j], kr[d + j], a[j]);
+      float val;
+      if (OVO_PLANT == 7) {
+        val = hsum8(a) * scale;
+      } else {
+        for (int j = 0; j < 8; ++j) a[j] = a[j] * scale;
+        val = hsum8(a);
+      }
+      if (br) val = val + br[t];
+      p[t] = val;
+      mx = val > mx ? val : mx;
+    }
+    float* orow = out + (int64_t)s * out_stride;
+    if (mx < -1e29f) {
+      for (int d = 0; d < D; ++d) orow[d] = 0.f;
+      continue;
+    }
+    float sumv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int i = 0;
+    for (; i + 8 <= S; i += 8)
+      for (int j = 0; j < 8; ++j) {
+        const float e = OVO_PLANT == 9 ? expf(p[i + j] - mx) : ovo_exp256(p[i + j] - mx);
+        p[i + j] = e;
+        sumv[j] = sumv[j] + e;
+      }
+    float sum = hsum8(sumv);
+    for (; i < S; ++i) {
+      const float e = expf(p[i] - mx);
+      p[i] = e;
+      sum = sum + e;
+    }
+    const float inv = 1.f / sum;
+    for (i = 0; i < S; ++i) p[i] = p[i] * inv;
+    for (int d = 0; d < D; ++d) {
+      float r = 0.f;
+      for (int t = 0; t < S; ++t) r = fmaf(p[t], v[(int64_t)t * kv_stride + d], r);
+      orow[d] = r;
+    }
+  }
+  free(p);
+  ftz_leave(csr);
+  return 0;
+}
+
+/* run_layer's attention loop (lm.cpp:259-276): for every segment and query head
+ * h, KV head h / (n_heads / n_kv_heads); offsets are element offsets into q/out
+ * (q_off) and k/v (kv_off); the output has the same layout as q. */
+OVO_API int ovo_attention(int n_segs, const float* const* bias, const int32_t* rows,
+                          const int64_t* q_off, const int64_t* kv_off, int n_heads,
+                          int n_kv_heads, int D, const float* q, const float* k, const float* v,
+                          float scale, float* out) {
+  if (n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return -1;
+  const int group = n_heads / n_kv_heads;
+  const int64_t QD = (int64_t)n_heads * D, KVD = (int64_t)n_kv_heads * D;
+  int rc = 0;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1) reduction(| : rc)
+  for (int s = 0; s < n_segs; ++s)
+    for (int h = 0; h < n_heads; ++h) {
+      const int kv = h / group;
+      rc |= ovo_attention_head(q + q_off[s] + (int64_t)h * D, QD, k + kv_off[s] + (int64_t)kv * D,
+                               v + kv_off[s] + (int64_t)kv * D, KVD, bias ? bias[s] : NULL,
+                               rows[s], D, scale, out + q_off[s] + (int64_t)h * D, QD);
+    }
+  return rc ? -1 : 0;
+}
+
+/* LM::embed (lm.cpp:180-198): row (b, s) with audio_mask set sums, from 0.f in
+ * codebook order, audio_emb[ids[b, c, s] + offsets[c]]; otherwise copies
+ * tok_emb[ids[b, 0, s]].  Tables are fp32 (tok_q/aud_q NULL) or int8 with one
+ * scale per row, gathered as (float)q * scale (mat.cpp:57-67).  Returns -1 on an
+ * id out of range (the reference throws). */
+OVO_API int ovo_embed(int batch, int seq, int C, int64_t H, const int64_t* ids,
+                      const uint8_t* mask, const float* tok_w, const int8_t* tok_q,
+                      const float* tok_s, int64_t tok_rows, const float* aud_w,
+                      const int8_t* aud_q, const float* aud_s, int64_t aud_rows,
+                      const int64_t* offsets, float* out) {
+  for (int b = 0; b < batch; ++b)
+    for (int s = 0; s < seq; ++s) {
+      const int64_t row = (int64_t)b * seq + s;
+      float* o = out + row * H;
+      if (mask[row]) {
+        for (int64_t h = 0; h < H; ++h) o[h] = 0.f;
+        for (int c = 0; c < C; ++c) {
+          const int64_t id = ids[((int64_t)b * C + c) * seq + s] + offsets[c];
+          if (id < 0 || id >= aud_rows) return -1;
+          for (int64_t h = 0; h < H; ++h) {
+            const float e = aud_w ? aud_w[id * H + h] : (float)aud_q[id * H + h] * aud_s[id];
+            o[h] = o[h] + e;
+          }
+        }
+      } else {
+        const int64_t id = ids[(int64_t)b * C * seq + s];
+        if (id < 0 || id >= tok_rows) return -1;
+        for (int64_t h = 0; h < H; ++h)
+          o[h] = tok_w ? tok_w[id * H + h] : (float)tok_q[id * H + h] * tok_s[id];
+      }
+    }
+  return 0;
 }

@@ -48,7 +48,17 @@ SIGNATURES = {
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
+    "ovh_rope_tables": (_int, [_i64, _p, _int, _f32, _p, _p, _p]),
+    "ovh_qk_norm_rope": (_int, [_p, _p, _p, _p, _i64, _int, _int, _int, _p, _p, _f32, _p]),
+    "ovh_attention": (_int, [_p, _int, _int, _int, _int, _p, _i64, _p, _p, _i64, _f32, _p,
+                             _i64, _p]),
 }
+
+
+class AttnSegment(C.Structure):
+    """OvhAttnSegment (same fields as ov::AttnSegment, cpp/src/model/lm.h:46-51)."""
+    _fields_ = [("bias", C.c_void_p), ("rows", C.c_int32), ("q_off", C.c_int64),
+                ("kv_off", C.c_int64)]
 
 
 class OvhError(RuntimeError):
@@ -255,4 +265,47 @@ def block_dots(aq, w: Weight):
     M = aq.shape[0]
     out = torch.empty((M, w.N, w.Kb), dtype=torch.int32, device="cuda")
     _check(load().ovh_block_dots(M, _dptr(aq), w.handle, _dptr(out), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# attention side of a decoder layer
+
+def rope_tables(pos, head_dim: int, theta: float = 1e6):
+    """cos/sin [rows, head_dim/2] for device int64 positions."""
+    torch = _torch()
+    pos = pos.contiguous()
+    c = torch.empty(pos.numel(), head_dim // 2, dtype=torch.float32, device=pos.device)
+    s = torch.empty_like(c)
+    _check(load().ovh_rope_tables(pos.numel(), _dptr(pos), head_dim, theta, _dptr(c), _dptr(s),
+                                  _stream()))
+    return c, s
+
+
+def qk_norm_rope(q, k, qw, kw, n_heads: int, n_kv_heads: int, head_dim: int, cos_tab, sin_tab,
+                 eps: float = 1e-6) -> None:
+    """In place on q [rows, n_heads*D] and k [rows, n_kv_heads*D] (qk_norm_rope_f32)."""
+    _check(load().ovh_qk_norm_rope(_dptr(q), _dptr(k), _dptr(qw), _dptr(kw), q.shape[0], n_heads,
+                                   n_kv_heads, head_dim, _dptr(cos_tab), _dptr(sin_tab), eps,
+                                   _stream()))
+
+
+def attention(q, k, v, segs, n_heads: int, n_kv_heads: int, head_dim: int = 128, scale=None,
+              out=None):
+    """GQA attention over segments (LM::run_layer's loop over attention_head_f32).
+
+    segs: list of (bias tensor [rows, rows] or None, rows, q_row0, kv_row0) with row
+    offsets into q [T, n_heads*D] and k/v [T, n_kv_heads*D]."""
+    torch = _torch()
+    if scale is None:
+        scale = float(torch.tensor(1.0) / torch.sqrt(torch.tensor(float(head_dim))))
+    if out is None:
+        out = torch.zeros_like(q)
+    arr = (AttnSegment * max(1, len(segs)))()
+    for i, (bias, rows, qr, kr) in enumerate(segs):
+        arr[i] = AttnSegment(0 if bias is None else _dptr(bias).value, rows,
+                             qr * q.stride(0), kr * k.stride(0))
+    _check(load().ovh_attention(C.cast(arr, C.c_void_p), len(segs), n_heads, n_kv_heads,
+                                head_dim, _dptr(q), q.stride(0), _dptr(k), _dptr(v), k.stride(0),
+                                scale, _dptr(out), out.stride(0), _stream()))
     return out

@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libovnative_amd.so")
-SOURCES = ["quant.hip", "gemm.hip", "capi.hip"]
+SOURCES = ["quant.hip", "gemm.hip", "attn.hip", "capi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [

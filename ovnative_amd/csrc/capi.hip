@@ -11,6 +11,7 @@
 #include <string>
 
 #include "../../include/ovnative_amd.h"
+#include "attn.h"
 #include "gemm.h"
 #include "ovh_common.h"
 #include "quant.h"
@@ -334,6 +335,72 @@ int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out
   a.start[1] = (int)w->w.N;
   a.dump = out;
   OVH_HIP(ovh::launch_gemm(a, ovh::kDumpBlocks, as_stream(stream)), "gemm launch");
+  return OV_OK;
+}
+
+
+int ovh_rope_tables(int64_t rows, const int64_t* pos, int head_dim, float theta, float* cos_tab,
+                    float* sin_tab, void* stream) {
+  if (rows <= 0) return OV_OK;
+  if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 1024)
+    return fail(OV_ERR_INVALID_ARG, "rope_tables: head_dim must be even and <= 1024");
+  if (!pos || !cos_tab || !sin_tab) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  OVH_HIP(ovh::launch_rope_tables(rows, pos, head_dim, theta, cos_tab, sin_tab, as_stream(stream)),
+          "rope tables launch");
+  return OV_OK;
+}
+
+int ovh_qk_norm_rope(float* q, float* k, const float* qw, const float* kw, int64_t rows,
+                     int n_heads, int n_kv_heads, int head_dim, const float* cos_tab,
+                     const float* sin_tab, float eps, void* stream) {
+  if (rows <= 0) return OV_OK;
+  if (head_dim != 64 && head_dim != 128)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "qk_norm_rope: head_dim must be 64 or 128");
+  if (n_heads < 0 || n_kv_heads < 0 || n_heads + n_kv_heads <= 0)
+    return fail(OV_ERR_INVALID_ARG, "qk_norm_rope: bad head counts");
+  if ((n_heads && (!q || !qw)) || (n_kv_heads && (!k || !kw)) || !cos_tab || !sin_tab)
+    return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  OVH_HIP(ovh::launch_qk_norm_rope(q, k, qw, kw, rows, n_heads, n_kv_heads, head_dim, cos_tab,
+                                   sin_tab, eps, as_stream(stream)),
+          "qk_norm_rope launch");
+  return OV_OK;
+}
+
+int ovh_attention(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_heads,
+                  int head_dim, const float* q, int64_t q_stride, const float* k, const float* v,
+                  int64_t kv_stride, float scale, float* out, int64_t out_stride, void* stream) {
+  if (n_segs <= 0) return OV_OK;
+  if (!segs) return fail(OV_ERR_INVALID_ARG, "segs is null");
+  if (head_dim != 128) return fail(OV_ERR_NOT_IMPLEMENTED, "attention: head_dim must be 128");
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 65535)
+    return fail(OV_ERR_INVALID_ARG, "attention: n_heads must be a positive multiple of n_kv_heads");
+  if (!q || !k || !v || !out) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (q_stride < (int64_t)n_heads * head_dim || out_stride < (int64_t)n_heads * head_dim ||
+      kv_stride < (int64_t)n_kv_heads * head_dim)
+    return fail(OV_ERR_INVALID_ARG, "attention: row strides smaller than the head span");
+  if ((q_stride | kv_stride | out_stride) & 3)
+    return fail(OV_ERR_INVALID_ARG, "attention: strides must be multiples of 4 elements");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u)
+    return fail(OV_ERR_INVALID_ARG, "attention: q/k/v/out must be 16-byte aligned");
+  for (int s = 0; s < n_segs; ++s) {
+    if (segs[s].rows < 0 || segs[s].q_off < 0 || segs[s].kv_off < 0 || (segs[s].q_off & 3) ||
+        (segs[s].kv_off & 3))
+      return fail(OV_ERR_INVALID_ARG, "attention: bad segment (rows/offsets)");
+  }
+  for (int s0 = 0; s0 < n_segs; s0 += ovh::kAttnMaxSegs) {
+    ovh::AttnArgs a{};
+    a.q = q; a.k = k; a.v = v; a.out = out;
+    a.q_stride = q_stride; a.kv_stride = kv_stride; a.out_stride = out_stride;
+    a.n_heads = n_heads; a.group = n_heads / n_kv_heads; a.scale = scale;
+    a.n_segs = n_segs - s0 < ovh::kAttnMaxSegs ? n_segs - s0 : ovh::kAttnMaxSegs;
+    int max_rows = 0;
+    for (int i = 0; i < a.n_segs; ++i) {
+      const OvhAttnSegment& g = segs[s0 + i];
+      a.segs[i] = ovh::AttnSeg{g.bias, g.rows, g.q_off, g.kv_off};
+      max_rows = g.rows > max_rows ? g.rows : max_rows;
+    }
+    OVH_HIP(ovh::launch_attention(a, max_rows, as_stream(stream)), "attention launch");
+  }
   return OV_OK;
 }
 

@@ -104,6 +104,35 @@ def main() -> None:
     for j, (w, s_, o) in enumerate(zip(Ws, ss, outs)):
         out[f"sl_W{j}"], out[f"sl_s{j}"], out[f"sl_C{j}"] = w, s_, o
 
+    # -- qk_norm_rope_f32 (ops_cpu.cpp:945-1016, tables built from positions) ------
+    for i, (rows, nh, nkv, D) in enumerate([(5, 4, 2, 128), (3, 2, 1, 64), (4, 16, 8, 128)]):
+        q = (rng.standard_normal((rows, nh * D)) * rng.uniform(0.5, 4.0)).astype(np.float32)
+        k = rng.standard_normal((rows, nkv * D)).astype(np.float32)
+        qw = rng.uniform(0.3, 1.7, D).astype(np.float32)
+        kw = rng.uniform(0.3, 1.7, D).astype(np.float32)
+        pos = rng.integers(0, 4000, rows).astype(np.int64)
+        pos[0] = 0                                  # cos 1, sin 0: the norm alone
+        qo, ko = ref.qk_norm_rope(q, k, qw, kw, nh, nkv, D, pos, 1e6, 1e-6)
+        for name, arr in dict(q=q, k=k, qw=qw, kw=kw, pos=pos, qo=qo, ko=ko).items():
+            out[f"qknr{i}_{name}"] = arr
+        out[f"qknr{i}_dims"] = np.array([rows, nh, nkv, D], np.int64)
+
+    # -- attention_head_f32 (ops_cpu.cpp:907-943 -> :586-786) ----------------------
+    acases = [(1, 128, 1.0, False), (7, 128, 1.0, True), (33, 128, 3.0, True),
+              (70, 128, 12.0, False), (19, 64, 1.0, True)]
+    for i, (S, D, mag, masked) in enumerate(acases):
+        q = (rng.standard_normal((S, D)) * mag).astype(np.float32)
+        k = rng.standard_normal((S, D)).astype(np.float32)
+        v = rng.standard_normal((S, D)).astype(np.float32)
+        bias = np.zeros((S, S), np.float32)
+        if masked:
+            bias[rng.random((S, S)) < 0.4] = -1e30
+            bias[0, :] = -1e30                      # a fully masked row -> zeros
+        o = ref.attention_head(q, k, v, bias if masked else None)
+        for name, arr in dict(q=q, k=k, v=v, bias=bias, out=o).items():
+            out[f"attn{i}_{name}"] = arr
+        out[f"attn{i}_masked"] = np.array(int(masked), np.int64)
+
     path = os.path.join(HERE, "int8nk_golden.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path)} bytes")

@@ -273,6 +273,18 @@ def golden_mismatches(o, golden):
     q, sc = o.quantize_weight_rows(golden["c1_Wf"])
     if not (np.array_equal(q, golden["c1_q"]) and np.array_equal(bits(sc), bits(golden["c1_s"]))):
         bad.append("c1")
+    for c in _cases(golden, "qknr"):
+        rows, nh, nkv, D = (int(x) for x in golden[c + "_dims"])
+        qo, ko = o.qk_norm_rope(golden[c + "_q"], golden[c + "_k"], golden[c + "_qw"],
+                                golden[c + "_kw"], nh, nkv, D, golden[c + "_pos"])
+        if not (np.array_equal(bits(qo), bits(golden[c + "_qo"])) and
+                np.array_equal(bits(ko), bits(golden[c + "_ko"]))):
+            bad.append(c)
+    for c in _cases(golden, "attn"):
+        bias = golden[c + "_bias"] if int(golden[c + "_masked"]) else None
+        out = o.attention_head(golden[c + "_q"], golden[c + "_k"], golden[c + "_v"], bias)
+        if not np.array_equal(bits(out), bits(golden[c + "_out"])):
+            bad.append(c)
     return bad
 
 
@@ -286,7 +298,7 @@ def test_weight_scale_floor(oracle):
     assert np.all(s == np.float32(1e-12)) and np.all(q == 0)
 
 
-@pytest.mark.parametrize("plant", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("plant", [1, 2, 3, 4, 5, 7, 8, 9])
 def test_planted_mistakes_are_caught(golden, plant, tmp_path):
     """Rebuild the oracle with one deliberate, plausible mistake (OVO_PLANT in
     oracle/ovoracle.c) and check that the golden vectors reject it."""

@@ -1,0 +1,165 @@
+"""CPU pins for the oracle's attention-side restatements (qk-norm + RoPE,
+attention, embedding): golden vectors from the compiled reference, the live
+reference where it is built, and properties the mathematics fixes."""
+import numpy as np
+import pytest
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.int32)
+
+
+def _cases(golden, prefix):
+    return sorted({k.split("_")[0] for k in golden if k.startswith(prefix)})
+
+
+def test_qk_norm_rope_golden(golden, oracle):
+    for c in _cases(golden, "qknr"):
+        rows, nh, nkv, D = (int(x) for x in golden[c + "_dims"])
+        qo, ko = oracle.qk_norm_rope(golden[c + "_q"], golden[c + "_k"], golden[c + "_qw"],
+                                     golden[c + "_kw"], nh, nkv, D, golden[c + "_pos"])
+        assert np.array_equal(bits(qo), bits(golden[c + "_qo"])), c
+        assert np.array_equal(bits(ko), bits(golden[c + "_ko"])), c
+
+
+def test_attention_golden(golden, oracle):
+    for c in _cases(golden, "attn"):
+        bias = golden[c + "_bias"] if int(golden[c + "_masked"]) else None
+        out = oracle.attention_head(golden[c + "_q"], golden[c + "_k"], golden[c + "_v"], bias)
+        assert np.array_equal(bits(out), bits(golden[c + "_out"])), c
+
+
+@pytest.mark.parametrize("S,D,mag", [(5, 128, 1.0), (64, 128, 8.0), (300, 128, 1.0),
+                                     (41, 64, 2.0), (9, 16, 1.0)])
+def test_attention_against_reference(reference, oracle, S, D, mag):
+    rng = np.random.default_rng(S * 7 + D)
+    q = (rng.standard_normal((S, D)) * mag).astype(np.float32)
+    k = rng.standard_normal((S, D)).astype(np.float32)
+    v = rng.standard_normal((S, D)).astype(np.float32)
+    bias = np.where(rng.random((S, S)) < 0.3, -1e30, 0.0).astype(np.float32)
+    bias[-1] = -1e30
+    for b in (None, bias):
+        assert np.array_equal(bits(oracle.attention_head(q, k, v, b)),
+                              bits(reference.attention_head(q, k, v, b)))
+
+
+def test_qk_norm_rope_against_reference(reference, oracle):
+    rng = np.random.default_rng(5)
+    rows, nh, nkv, D = 40, 16, 8, 128
+    q = (rng.standard_normal((rows, nh * D)) * 2).astype(np.float32)
+    k = rng.standard_normal((rows, nkv * D)).astype(np.float32)
+    qw = rng.uniform(0.2, 2.0, D).astype(np.float32)
+    kw = rng.uniform(0.2, 2.0, D).astype(np.float32)
+    pos = rng.integers(0, 20000, rows)
+    a = oracle.qk_norm_rope(q, k, qw, kw, nh, nkv, D, pos)
+    b = reference.qk_norm_rope(q, k, qw, kw, nh, nkv, D, pos)
+    assert np.array_equal(bits(a[0]), bits(b[0])) and np.array_equal(bits(a[1]), bits(b[1]))
+
+
+def test_rope_tables_closed_form(oracle):
+    """inv_freq = theta^(-2i/D); pos 0 gives cos 1, sin 0; every entry is within
+    one ulp of cos/sin of the float angle evaluated in double."""
+    pos = np.array([0, 1, 7, 299, 1023, 40000], np.int64)
+    D, theta = 128, 1e6
+    c, s = oracle.rope_tables(pos, D, theta)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+    inv = (theta ** (-2.0 * np.arange(D // 2) / D)).astype(np.float32)
+    ang = pos.astype(np.float32)[:, None] * inv[None, :]
+    for got, fn in ((c, np.cos), (s, np.sin)):
+        want = fn(ang.astype(np.float64)).astype(np.float32)
+        assert np.abs(bits(got).astype(np.int64) - bits(want).astype(np.int64)).max() <= 1
+
+
+def test_qk_norm_rope_properties(oracle):
+    """At pos 0 the rotation is the identity, so the output is the per-head norm
+    alone; at any position each (i, i+D/2) pair keeps its length."""
+    rng = np.random.default_rng(11)
+    rows, nh, nkv, D = 3, 2, 1, 128
+    q = rng.standard_normal((rows, nh * D)).astype(np.float32)
+    k = rng.standard_normal((rows, nkv * D)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    qo, _ = oracle.qk_norm_rope(q, k, w, w, nh, nkv, D, np.zeros(rows, np.int64))
+    x = q.reshape(rows, nh, D).astype(np.float64)
+    ref = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(qo.reshape(rows, nh, D), ref, rtol=2e-6, atol=1e-7)
+    qo, _ = oracle.qk_norm_rope(q, k, w, w, nh, nkv, D, np.array([5, 77, 3000]))
+    y = qo.reshape(rows, nh, D).astype(np.float64)
+    h = D // 2
+    np.testing.assert_allclose(y[..., :h] ** 2 + y[..., h:] ** 2,
+                               ref[..., :h] ** 2 + ref[..., h:] ** 2, rtol=1e-5, atol=1e-9)
+
+
+def test_attention_properties(oracle):
+    """One visible key returns that key's value row; q = 0 gives the mean of V;
+    a fully masked row is zero."""
+    rng = np.random.default_rng(3)
+    S, D = 37, 128
+    q = rng.standard_normal((S, D)).astype(np.float32)
+    k = rng.standard_normal((S, D)).astype(np.float32)
+    v = rng.standard_normal((S, D)).astype(np.float32)
+    bias = np.full((S, S), -1e30, np.float32)
+    pick = rng.integers(0, S, S)
+    bias[np.arange(S), pick] = 0.0
+    bias[5] = -1e30
+    out = oracle.attention_head(q, k, v, bias)
+    rows = np.arange(S) != 5
+    np.testing.assert_allclose(out[rows], v[pick[rows]], rtol=1e-7, atol=1e-30)
+    assert np.all(out[5] == 0.0)
+    out = oracle.attention_head(np.zeros_like(q), k, v)
+    np.testing.assert_allclose(out, np.broadcast_to(v.astype(np.float64).mean(0), (S, D)),
+                               rtol=0, atol=2e-6)
+
+
+def test_attention_gqa_loop(oracle):
+    """The multi-segment GQA driver equals per-head calls (KV head = h / group)."""
+    rng = np.random.default_rng(4)
+    nh, nkv, D = 4, 2, 64
+    segs_rows = [9, 6]
+    T = sum(segs_rows)
+    q = rng.standard_normal((T, nh * D)).astype(np.float32)
+    k = rng.standard_normal((T, nkv * D)).astype(np.float32)
+    v = rng.standard_normal((T, nkv * D)).astype(np.float32)
+    b1 = np.where(rng.random((6, 6)) < 0.3, -1e30, 0).astype(np.float32)
+    segs = [(None, 9, 0, 0), (b1, 6, 9, 9)]
+    out = oracle.attention(q, k, v, segs, nh, nkv, D)
+    for bias, rows, r0, _ in segs:
+        for h in range(nh):
+            kv = h // (nh // nkv)
+            want = oracle.attention_head(q[r0:r0 + rows, h * D:(h + 1) * D],
+                                         k[r0:r0 + rows, kv * D:(kv + 1) * D],
+                                         v[r0:r0 + rows, kv * D:(kv + 1) * D], bias)
+            assert np.array_equal(bits(out[r0:r0 + rows, h * D:(h + 1) * D]), bits(want))
+
+
+def test_embed_brute_force(oracle):
+    rng = np.random.default_rng(8)
+    B, Cb, S, H, V = 2, 8, 6, 32, 11
+    tok = rng.standard_normal((50, H)).astype(np.float32)
+    aud = rng.standard_normal((Cb * V, H)).astype(np.float32)
+    offs = np.arange(Cb, dtype=np.int64) * V
+    ids = rng.integers(0, V, (B, Cb, S)).astype(np.int64)
+    mask = (rng.random((B, S)) < 0.5).astype(np.uint8)
+    out = oracle.embed(ids, mask, tok, aud, offs)
+    for b in range(B):
+        for s in range(S):
+            if mask[b, s]:
+                acc = np.zeros(H, np.float32)
+                for c in range(Cb):
+                    acc = (acc + aud[ids[b, c, s] + offs[c]]).astype(np.float32)
+                want = acc
+            else:
+                want = tok[ids[b, 0, s]]
+            assert np.array_equal(bits(out[b * S + s]), bits(want))
+    # int8 tables with per-row scales: gathered as float(q) * scale
+    tq = rng.integers(-127, 128, tok.shape).astype(np.int8)
+    ts = rng.uniform(1e-3, 1e-2, tok.shape[0]).astype(np.float32)
+    aq = rng.integers(-127, 128, aud.shape).astype(np.int8)
+    as_ = rng.uniform(1e-3, 1e-2, aud.shape[0]).astype(np.float32)
+    out = oracle.embed(ids, mask, tq, aq, offs, ts, as_)
+    b, s = np.argwhere(mask == 0)[0]
+    assert np.array_equal(bits(out[b * S + s]),
+                          bits(tq[ids[b, 0, s]].astype(np.float32) * ts[ids[b, 0, s]]))
+    with pytest.raises(ValueError):
+        bad = ids.copy()
+        bad[0, 0, :] = 10_000
+        oracle.embed(bad, np.zeros_like(mask), tok, aud, offs)
