@@ -171,6 +171,86 @@ int ovh_attention(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_
                   int head_dim, const float* q, int64_t q_stride, const float* k, const float* v,
                   int64_t kv_stride, float scale, float* out, int64_t out_stride, void* stream);
 
+/* ---- weights: OVW1 files -------------------------------------------------- */
+
+/* A tensor of a checkpoint: same fields as ov::Tensor
+ * (cpp/include/ovnative/ov_types.h).  dtype: 0 f32, 1 i8, 2 f16, 3 i64 (ov::DType);
+ * transposed = OVW1 layout 1 (2-D linear weight stored [in, out]); quantized =
+ * per-output-channel int8 with n_scales fp32 scales.  data/scales are HOST memory. */
+typedef struct OvhTensorView {
+  const char* name;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t dims[4];
+  int32_t transposed;
+  int32_t quantized;
+  const void* data;
+  int64_t nbytes;
+  const float* scales;
+  int64_t n_scales;
+  uint32_t crc;
+} OvhTensorView;
+
+typedef struct OvhWeightFile OvhWeightFile;
+
+/* WeightFile::Open (ov_weights.h:29, weight_file.cpp): mmap an OVW1 file and
+ * check it the way the reference loader does (magic, version, file size, index,
+ * names, payload and scale bounds, byte size = shape x dtype).  Format errors
+ * return OV_ERR_IO (the reference throws std::runtime_error). */
+int ovh_ovw1_open(const char* path, OvhWeightFile** out);
+void ovh_ovw1_close(OvhWeightFile* wf);
+/* tensors() / Find() / n_params() (ov_weights.h:36-43); views live until close. */
+int ovh_ovw1_count(const OvhWeightFile* wf);
+const OvhTensorView* ovh_ovw1_tensors(const OvhWeightFile* wf);
+const OvhTensorView* ovh_ovw1_find(const OvhWeightFile* wf, const char* name);
+uint64_t ovh_ovw1_n_params(const OvhWeightFile* wf);
+/* ComputeCrc (ov_weights.h:45): CRC-32 of tensor `index`'s payload, to compare
+ * with the stored OvhTensorView.crc. */
+uint32_t ovh_ovw1_compute_crc(const OvhWeightFile* wf, int index);
+
+/* ---- LM runner: the accelerator plugin of cpp/src/backend/cuda/cuda_lm.h ------ */
+
+/* ov::LMConfig (cpp/src/model/lm.h:17-29). */
+typedef struct OvhLmConfig {
+  int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, inter, vocab, audio_vocab,
+      n_codebooks;
+  float rms_eps, rope_theta;
+} OvhLmConfig;
+
+typedef struct OvhLm OvhLm;
+
+/* LmRunnerCreate (cuda_lm.h:31): uploads the LM's tensors (the reference's names,
+ * lm.cpp:96-149) and merges q/k/v and gate/up.  Linear weights must be int8 with
+ * per-channel scales, OVW1 layout 0 or 1; embeddings fp32 or int8.  All work is
+ * enqueued on `stream` (hipStream_t), which the runner keeps using.  Returns
+ * OV_ERR_NOT_IMPLEMENTED for configurations the HIP kernels do not cover (the
+ * reference's factory returns null and the caller stays on the CPU). */
+int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_tensors,
+                  void* stream, OvhLm** out);
+/* LmRunnerDelete. */
+void ovh_lm_destroy(OvhLm* lm);
+/* LmRunnerForward / LmRunnerForwardThunk (cuda_lm.h:34-36, :50-52) = LM::forward
+ * (lm.h:65-73): host inputs ids [B, 8, S] int64, audio_mask [B, S], attn_mask
+ * [B, S, S] (1 = attend), position_ids [B, S]; logits host [B, C, S, V], or NULL
+ * (or device sampling on) to leave them on the device only. */
+int ovh_lm_forward(OvhLm* lm, int batch, int seq, const int64_t* input_ids,
+                   const uint8_t* audio_mask, const uint8_t* attn_mask,
+                   const int64_t* position_ids, float* logits);
+/* LM::forward_cfg (lm.h:75-82): ragged CFG batch, cond_seq rows then uncond_seq
+ * rows; ids [C, rows] codebook-major, logits host [rows, C*V] token-major (or NULL). */
+int ovh_lm_forward_cfg(OvhLm* lm, int cond_seq, int uncond_seq, const int64_t* input_ids,
+                       const uint8_t* audio_mask, const uint8_t* cond_attn,
+                       const uint8_t* uncond_attn, const int64_t* position_ids, float* logits);
+/* LmRunnerLastLogitsThunk (cuda_lm.h:42): device logits [rows, C*V] of the last forward. */
+const void* ovh_lm_last_logits(const OvhLm* lm);
+/* LmRunnerSetDeviceSampling (cuda_lm.h:46). */
+void ovh_lm_set_device_sampling(OvhLm* lm, int on);
+/* LmRunnerSampleThunk (cuda_lm.h:39-41): the per-step guidance + argmax pass
+ * (tts.cpp:296-326) on device logit planes; pred/scores host [C, target_len]. */
+int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,
+                  int target_len, float guidance, float layer_penalty, int32_t* pred,
+                  float* scores);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

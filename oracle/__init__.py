@@ -84,6 +84,8 @@ class Oracle:
                                         _p, _p, _f32, _p]),
             "ovo_embed": (C.c_int, [C.c_int, C.c_int, C.c_int, _i64, _p, _p, _p, _p, _p, _i64, _p,
                                     _p, _p, _i64, _p, _p]),
+            "ovo_guided_sample": (C.c_int, [_p, C.c_int, _p, C.c_int, C.c_int, C.c_int, _f32, _f32,
+                                            C.c_int, C.c_int, _p, _p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -276,6 +278,80 @@ class Oracle:
             raise ValueError("embed: id out of range")
         return out
 
+    def guided_sample(self, cond, cond_seq, uncond, C_, V, target_len, guidance, layer_penalty,
+                      mask_id=None, cpu_alias=False):
+        """cond [cond_seq, C*V], uncond [>= target_len, C*V] token-major logit planes.
+        cpu_alias=True reproduces tts.cpp's in-place log_softmax quirk (host path);
+        the default is the device sampler's arithmetic (cuda_lm.cu:720-756)."""
+        cond = np.ascontiguousarray(cond, dtype=np.float32)
+        uncond = np.ascontiguousarray(uncond, dtype=np.float32)
+        n = C_ * target_len
+        pred = np.empty(n, np.int32)
+        scores = np.empty(n, np.float32)
+        rc = self.lib.ovo_guided_sample(_ptr(cond), cond_seq, _ptr(uncond), C_, V, target_len,
+                                        guidance, layer_penalty, V - 1 if mask_id is None else mask_id,
+                                        int(bool(cpu_alias)), _ptr(pred), _ptr(scores))
+        if rc != 0:
+            raise ValueError("guided_sample: bad sizes")
+        return pred.reshape(C_, target_len), scores.reshape(C_, target_len)
+
+    # -- the LM forward, composed from the restated pieces ------------------
+    def _linear_fast(self, aq, asc, W, wscale, C=None, accumulate=False):
+        """linear_q through the AVX-512 VNNI form when the host has it (same bits,
+        tests/test_oracle.py::test_fast_path_matches_scalar)."""
+        if not self.fast_available():
+            return self.linear_q(aq, asc, W, wscale, C, accumulate)
+        N, K = W.shape
+        packed, wsum = self.pack(W)
+        out = np.zeros((aq.shape[0], N), np.float32) if C is None else \
+            np.array(C, dtype=np.float32, copy=True, order="C")
+        return self.linear_q_packed(aq, asc, packed, wsum, N, K,
+                                    np.ascontiguousarray(wscale, dtype=np.float32), out, accumulate)
+
+    def lm_forward(self, cfg, tensors, ids, audio_mask, segs, pos, attention=None):
+        """LM::run_layer / forward (cpp/src/model/lm.cpp:217-401) on the int8-nk
+        path: `tensors` maps the reference's tensor names to (array, scales,
+        transposed); ids [B, C, S]; segs = [(mask [rows, rows] u8 or None, rows,
+        row0)]; pos [T].  Returns logits [T, C*V] token-major.  `attention`, if
+        given, replaces the attention step: attention(q, k, v, segs) -> out (the
+        tests pass the device kernel here to isolate every other step)."""
+        g = lambda n: tensors[n]
+
+        def lin(name):
+            a, sc, tr = g(name)
+            return (np.ascontiguousarray(a.T) if tr else a), sc
+
+        H, NH, NKV, D = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+        eps, theta = cfg.get("rms_eps", 1e-6), cfg.get("rope_theta", 1e6)
+        tok, tok_s, _ = g("llm.embed_tokens.weight")
+        aud, aud_s, _ = g("audio_embeddings.weight")
+        offs = g("codebook_layer_offsets")[0]
+        x = self.embed(ids, audio_mask, tok, aud, offs, tok_s, aud_s)
+        tables = self.rope_tables(pos, D, theta)
+        asegs = [(None if m is None else np.where(m != 0, 0.0, -1e30).astype(np.float32), r, r0, r0)
+                 for m, r, r0 in segs]
+        for li in range(cfg["n_layers"]):
+            p = f"llm.layers.{li}."
+            aq, asc = self.rmsnorm_quantize(x, g(p + "input_layernorm.weight")[0], eps)
+            lq = self._linear_fast
+            q = lq(aq, asc, *lin(p + "self_attn.q_proj.weight"))
+            k = lq(aq, asc, *lin(p + "self_attn.k_proj.weight"))
+            v = lq(aq, asc, *lin(p + "self_attn.v_proj.weight"))
+            q, k = self.qk_norm_rope(q, k, g(p + "self_attn.q_norm.weight")[0],
+                                     g(p + "self_attn.k_norm.weight")[0], NH, NKV, D, eps=eps,
+                                     tables=tables)
+            att = (self.attention(q, k, v, asegs, NH, NKV, D) if attention is None
+                   else attention(q, k, v, asegs))
+            aq, asc = self.quantize(att)
+            x = lq(aq, asc, *lin(p + "self_attn.o_proj.weight"), C=x, accumulate=True)
+            aq, asc = self.rmsnorm_quantize(x, g(p + "post_attention_layernorm.weight")[0], eps)
+            gate = lq(aq, asc, *lin(p + "mlp.gate_proj.weight"))
+            up = lq(aq, asc, *lin(p + "mlp.up_proj.weight"))
+            aq, asc = self.silu_mul_quantize(gate, up)
+            x = lq(aq, asc, *lin(p + "mlp.down_proj.weight"), C=x, accumulate=True)
+        aq, asc = self.rmsnorm_quantize(x, g("llm.norm.weight")[0], eps)
+        return self._linear_fast(aq, asc, *lin("audio_heads.weight"))
+
 
 class Reference:
     """The reference's compiled CPU kernels (see ``oracle/ref_shim.cpp``)."""
@@ -305,6 +381,10 @@ class Reference:
                                           _f32, _f32]),
             "ovref_attention_head": (None, [_p, _i64, _p, _p, _i64, _p, C.c_int, C.c_int, _f32,
                                             _p, _i64]),
+            "ovref_ovw1_open": (_p, [C.c_char_p, C.c_char_p, C.c_size_t]),
+            "ovref_ovw1_close": (None, [_p]),
+            "ovref_ovw1_count": (C.c_int, [_p]),
+            "ovref_ovw1_get": (C.c_int, [_p, C.c_char_p] + [_p] * 11),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -313,6 +393,40 @@ class Reference:
 
     def vnni_available(self) -> bool:
         return bool(self.lib.ovref_vnni_available())
+
+    def ovw1_read(self, path, names):
+        """Open `path` with the reference loader (WeightFile::Open); returns
+        (n_tensors, {name: dict(dtype, dims, transposed, quantized, data bytes,
+        scales, stored_crc, computed_crc)}).  Raises RuntimeError with the
+        loader's message on a format error."""
+        err = C.create_string_buffer(512)
+        h = self.lib.ovref_ovw1_open(os.fsencode(path), err, 512)
+        if not h:
+            raise RuntimeError(err.value.decode())
+        try:
+            out = {}
+            for name in names:
+                dt, nd, tr, qu = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+                dims = (C.c_int64 * 4)()
+                data, sc = C.c_void_p(), C.c_void_p()
+                nb, ns = C.c_int64(), C.c_int64()
+                scrc, ccrc = C.c_uint32(), C.c_uint32()
+                rc = self.lib.ovref_ovw1_get(h, name.encode(), C.byref(dt), C.byref(nd), dims,
+                                             C.byref(tr), C.byref(qu), C.byref(data), C.byref(nb),
+                                             C.byref(sc), C.byref(ns), C.byref(scrc),
+                                             C.byref(ccrc))
+                if rc != 0:
+                    out[name] = None
+                    continue
+                raw = C.string_at(data.value, nb.value) if nb.value else b""
+                scales = (np.frombuffer(C.string_at(sc.value, 4 * ns.value), np.float32).copy()
+                          if qu.value and ns.value else None)
+                out[name] = dict(dtype=dt.value, dims=tuple(dims[:nd.value]), transposed=tr.value,
+                                 quantized=qu.value, data=raw, scales=scales,
+                                 stored_crc=scrc.value, computed_crc=ccrc.value)
+            return self.lib.ovref_ovw1_count(h), out
+        finally:
+            self.lib.ovref_ovw1_close(h)
 
     def qk_norm_rope(self, q, k, qw, kw, n_heads, n_kv_heads, D, pos, theta=1e6, eps=1e-6):
         q = np.array(q, dtype=np.float32, copy=True, order="C")

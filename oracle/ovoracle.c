@@ -469,6 +469,8 @@ OVO_API int ovo_num_threads(void) {
  *                       per-row arithmetic), run under FTZ/DAZ like the reference
  *   ovo_attention       cpp/src/model/lm.cpp:259-276 (GQA loop over segments/heads)
  *   ovo_embed           cpp/src/model/lm.cpp:180-198, mat.cpp:57-67 (Emb::gather)
+ *   ovo_guided_sample   cpp/src/model/tts.cpp:91-101, 296-326 (parity unpinned against
+ *                       a reference binary; pinned by properties)
  * ====================================================================== */
 
 /* FTZ/DAZ as enable_flush_to_zero() sets them (ops_cpu.cpp:1132-1136). */
@@ -681,5 +683,74 @@ OVO_API int ovo_embed(int batch, int seq, int C, int64_t H, const int64_t* ids,
           o[h] = tok_w ? tok_w[id * H + h] : (float)tok_q[id * H + h] * tok_s[id];
       }
     }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------
+ * Guided sampling, cpp/src/model/tts.cpp:91-101 (log_softmax) and :296-326,
+ * per (codebook c, target frame t) on token-major planes [S, C*V]: cond at
+ * its last target_len positions, uncond at its first (the device form,
+ * cuda_lm.cu:679-690).  tts.cpp is compiled for baseline x86-64 (no FMA
+ * contraction), so every product and sum rounds on its own.
+ *
+ * cpu_alias = 1 reproduces the host path exactly, including that it calls
+ * log_softmax(lp_mix, V, lp_mix) in place: the function's last loop then reads
+ * x[i] after its second loop overwrote it with exp(x[i] - m), so the host's
+ * guided log-probabilities are exp(mix - m) - lse.  cpu_alias = 0 is the
+ * reference's device sampler (cuda_lm.cu:720-756), which an accelerator backend
+ * uses: mix - lse.  The argmax agrees except where exp() underflows to ties;
+ * the scores differ.  Parity unpinned against a reference binary (tts.cpp needs
+ * the whole pipeline to build); pinned by the properties in
+ * tests/test_oracle_layer.py.
+ * ---------------------------------------------------------------------- */
+static void log_softmax_row(const float* x, int n, float* out) {
+  float m = -INFINITY;
+  for (int i = 0; i < n; ++i) m = x[i] > m ? x[i] : m;
+  float sum = 0.f;
+  for (int i = 0; i < n; ++i) {
+    out[i] = expf(x[i] - m);
+    sum = sum + out[i];
+  }
+  const float lse = logf(sum) + m;
+  for (int i = 0; i < n; ++i) out[i] = x[i] - lse;
+}
+
+OVO_API int ovo_guided_sample(const float* cond, int cond_seq, const float* uncond, int C, int V,
+                              int target_len, float guidance, float layer_penalty, int mask_id,
+                              int cpu_alias, int32_t* pred, float* scores) {
+  if (target_len <= 0 || target_len > cond_seq || V <= 0) return -1;
+  const int64_t CV = (int64_t)C * V;
+  float* buf = (float*)malloc(sizeof(float) * 4 * (size_t)V);
+  if (!buf) return -1;
+  float *lp_c = buf, *lp_u = buf + V, *mix = buf + 2 * V, *tmp = buf + 3 * V;
+  for (int idx = 0; idx < C * target_len; ++idx) {
+    const int c = idx / target_len, t = idx - c * target_len;
+    const float* lc = cond + (int64_t)(cond_seq - target_len + t) * CV + (int64_t)c * V;
+    const float* lu = uncond + (int64_t)t * CV + (int64_t)c * V;
+    log_softmax_row(lc, V, lp_c);
+    log_softmax_row(lu, V, lp_u);
+    if (guidance != 0.f) {
+      for (int v = 0; v < V; ++v) mix[v] = lp_c[v] + guidance * (lp_c[v] - lp_u[v]);
+      if (cpu_alias) {
+        log_softmax_row(mix, V, mix);
+      } else {
+        log_softmax_row(mix, V, tmp);
+        memcpy(mix, tmp, sizeof(float) * (size_t)V);
+      }
+    } else {
+      memcpy(mix, lp_c, sizeof(float) * (size_t)V);
+    }
+    if (mask_id >= 0 && mask_id < V) mix[mask_id] = -INFINITY;
+    int best = 0;
+    float best_val = -INFINITY;
+    for (int v = 0; v < V; ++v)
+      if (mix[v] > best_val) {
+        best_val = mix[v];
+        best = v;
+      }
+    pred[idx] = best;
+    scores[idx] = best_val - (float)c * layer_penalty;
+  }
+  free(buf);
   return 0;
 }

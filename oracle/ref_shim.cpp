@@ -6,11 +6,13 @@
 // reference sources where they lie; nothing in the product loads it.
 // Exceptions thrown by the reference become negative return codes here.
 #include <cstdint>
+#include <cstdio>
 #include <stdexcept>
 #include <vector>
 
 #include "model/ops.h"
 #include "ovnative/ov_gemm.h"
+#include "ovnative/ov_weights.h"
 
 #define REF_API extern "C" __attribute__((visibility("default")))
 
@@ -87,4 +89,39 @@ REF_API void ovref_attention_head(const float* q, int64_t q_stride, const float*
                                   int64_t kv_stride, const float* bias, int S, int D, float scale,
                                   float* out, int64_t out_stride) {
   ov::attention_head_f32(q, q_stride, k, v, kv_stride, bias, S, D, scale, out, out_stride);
+}
+
+// OVW1 reader (cpp/src/core/weight_file.cpp): opens files written by
+// ovnative_amd/ovw1.py so the tests can check them against the reference loader.
+REF_API void* ovref_ovw1_open(const char* path, char* err, size_t n) {
+  try {
+    return new ov::WeightFile(ov::WeightFile::Open(path));
+  } catch (const std::exception& e) {
+    if (err && n) std::snprintf(err, n, "%s", e.what());
+    return nullptr;
+  }
+}
+REF_API void ovref_ovw1_close(void* h) { delete static_cast<ov::WeightFile*>(h); }
+REF_API int ovref_ovw1_count(void* h) {
+  return static_cast<int>(static_cast<ov::WeightFile*>(h)->tensors().size());
+}
+REF_API int ovref_ovw1_get(void* h, const char* name, int* dtype, int* ndim, int64_t* dims,
+                           int* transposed, int* quantized, const void** data, int64_t* nbytes,
+                           const float** scales, int64_t* n_scales, uint32_t* stored_crc,
+                           uint32_t* computed_crc) {
+  const auto* wf = static_cast<ov::WeightFile*>(h);
+  const ov::Tensor* t = wf->Find(name);
+  if (!t) return -1;
+  *dtype = static_cast<int>(t->dtype);
+  *ndim = t->shape.ndim;
+  for (int k = 0; k < 4; ++k) dims[k] = t->shape.dims[k];
+  *transposed = t->transposed ? 1 : 0;
+  *quantized = t->quantized ? 1 : 0;
+  *data = t->data;
+  *nbytes = t->nbytes;
+  *scales = t->scales;
+  *n_scales = t->n_scales;
+  *stored_crc = wf->StoredCrc(*t);
+  *computed_crc = wf->ComputeCrc(*t);
+  return 0;
 }

@@ -52,7 +52,43 @@ SIGNATURES = {
     "ovh_qk_norm_rope": (_int, [_p, _p, _p, _p, _i64, _int, _int, _int, _p, _p, _f32, _p]),
     "ovh_attention": (_int, [_p, _int, _int, _int, _int, _p, _i64, _p, _p, _i64, _f32, _p,
                              _i64, _p]),
+    "ovh_ovw1_open": (_int, [C.c_char_p, C.POINTER(_p)]),
+    "ovh_ovw1_close": (None, [_p]),
+    "ovh_ovw1_count": (_int, [_p]),
+    "ovh_ovw1_tensors": (_p, [_p]),
+    "ovh_ovw1_find": (_p, [_p, C.c_char_p]),
+    "ovh_ovw1_n_params": (C.c_uint64, [_p]),
+    "ovh_ovw1_compute_crc": (C.c_uint32, [_p, _int]),
+    "ovh_lm_create": (_int, [_p, _p, _int, _p, C.POINTER(_p)]),
+    "ovh_lm_destroy": (None, [_p]),
+    "ovh_lm_forward": (_int, [_p, _int, _int, _p, _p, _p, _p, _p]),
+    "ovh_lm_forward_cfg": (_int, [_p, _int, _int, _p, _p, _p, _p, _p, _p]),
+    "ovh_lm_last_logits": (_p, [_p]),
+    "ovh_lm_set_device_sampling": (None, [_p, _int]),
+    "ovh_lm_sample": (_int, [_p, _p, _int, _p, _int, _int, _f32, _f32, _p, _p]),
 }
+
+
+class TensorView(C.Structure):
+    """OvhTensorView (same fields as ov::Tensor, cpp/include/ovnative/ov_types.h)."""
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
+                ("dims", C.c_int64 * 4), ("transposed", C.c_int32), ("quantized", C.c_int32),
+                ("data", C.c_void_p), ("nbytes", C.c_int64), ("scales", C.c_void_p),
+                ("n_scales", C.c_int64), ("crc", C.c_uint32)]
+
+
+class LmConfig(C.Structure):
+    """OvhLmConfig = ov::LMConfig (cpp/src/model/lm.h:17-29); defaults are the reference's."""
+    _fields_ = [(n, C.c_int32) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                         "head_dim", "inter", "vocab", "audio_vocab",
+                                         "n_codebooks")] + \
+               [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+    def __init__(self, **kw):
+        d = dict(n_layers=28, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, inter=3072,
+                 vocab=151676, audio_vocab=1025, n_codebooks=8, rms_eps=1e-6, rope_theta=1e6)
+        d.update(kw)
+        super().__init__(**d)
 
 
 class AttnSegment(C.Structure):
@@ -309,3 +345,160 @@ def attention(q, k, v, segs, n_heads: int, n_kv_heads: int, head_dim: int = 128,
                                 head_dim, _dptr(q), q.stride(0), _dptr(k), _dptr(v), k.stride(0),
                                 scale, _dptr(out), out.stride(0), _stream()))
     return out
+
+
+# ---------------------------------------------------------------------------
+# OVW1 files and the LM runner
+
+class WeightFile:
+    """An mmapped OVW1 checkpoint (ovh_ovw1_open = WeightFile::Open)."""
+
+    def __init__(self, path: str):
+        lib = load()
+        h = C.c_void_p()
+        _check(lib.ovh_ovw1_open(os.fsencode(path), C.byref(h)))
+        self.handle = h
+        n = lib.ovh_ovw1_count(h)
+        base = lib.ovh_ovw1_tensors(h)
+        self.views = (TensorView * n).from_address(base) if n else (TensorView * 0)()
+
+    def __len__(self):
+        return len(self.views)
+
+    def names(self):
+        return [v.name.decode() for v in self.views]
+
+    def find(self, name: str):
+        p = load().ovh_ovw1_find(self.handle, name.encode())
+        return None if not p else TensorView.from_address(p)
+
+    def crc_ok(self) -> bool:
+        lib = load()
+        return all(lib.ovh_ovw1_compute_crc(self.handle, i) == v.crc
+                   for i, v in enumerate(self.views))
+
+    def close(self):
+        if self.handle:
+            load().ovh_ovw1_close(self.handle)
+            self.handle = None
+            self.views = (TensorView * 0)()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def views_from_tensors(tensors):
+    """TensorView array over host numpy arrays (ovw1.Tensor list); the returned
+    keepalive list must outlive the views."""
+    import numpy as np
+    dt = {np.dtype(np.float32): 0, np.dtype(np.int8): 1, np.dtype(np.float16): 2,
+          np.dtype(np.int64): 3}
+    arr = (TensorView * len(tensors))()
+    keep = []
+    for i, t in enumerate(tensors):
+        a = np.ascontiguousarray(t.array)
+        name = t.name.encode()
+        keep += [a, name]
+        v = arr[i]
+        v.name, v.dtype, v.ndim = name, dt[a.dtype], a.ndim
+        for k in range(a.ndim):
+            v.dims[k] = a.shape[k]
+        v.transposed = 1 if t.layout == 1 else 0
+        v.data, v.nbytes = a.ctypes.data, a.nbytes
+        if t.scales is not None:
+            sc = np.ascontiguousarray(t.scales, dtype=np.float32)
+            keep.append(sc)
+            v.quantized, v.scales, v.n_scales = 1, sc.ctypes.data, sc.size
+    return arr, keep
+
+
+class LM:
+    """The HIP LM runner (ovh_lm_* = the accelerator plugin of cuda_lm.h); all
+    work runs on torch's current stream at construction time."""
+
+    def __init__(self, cfg: LmConfig, views, n: int):
+        lib = load()
+        self.cfg = cfg
+        h = C.c_void_p()
+        _check(lib.ovh_lm_create(C.byref(cfg), C.cast(views, C.c_void_p), n, _stream(),
+                                 C.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_file(cls, path: str, cfg: LmConfig):
+        wf = WeightFile(path)
+        try:
+            return cls(cfg, wf.views, len(wf))
+        finally:
+            wf.close()
+
+    @classmethod
+    def from_tensors(cls, tensors, cfg: LmConfig):
+        views, keep = views_from_tensors(tensors)
+        lm = cls(cfg, views, len(tensors))
+        del keep
+        return lm
+
+    def forward(self, ids, audio_mask, attn_mask, pos, host_logits: bool = True):
+        """ids [B, C, S] int64, audio_mask [B, S] u8, attn_mask [B, S, S] u8, pos [B, S]
+        int64 (numpy); returns logits [B, C, S, V] (numpy) or None."""
+        import numpy as np
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        am = np.ascontiguousarray(audio_mask, dtype=np.uint8)
+        at = np.ascontiguousarray(attn_mask, dtype=np.uint8)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        B, Cb, S = ids.shape
+        out = np.empty((B, Cb, S, self.cfg.audio_vocab), np.float32) if host_logits else None
+        _check(load().ovh_lm_forward(self.handle, B, S, ids.ctypes.data, am.ctypes.data,
+                                     at.ctypes.data, pos.ctypes.data,
+                                     None if out is None else out.ctypes.data))
+        return out
+
+    def forward_cfg(self, cond_seq, uncond_seq, ids, audio_mask, cond_attn, uncond_attn, pos,
+                    host_logits: bool = True):
+        import numpy as np
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        am = np.ascontiguousarray(audio_mask, dtype=np.uint8)
+        ca = np.ascontiguousarray(cond_attn, dtype=np.uint8)
+        ua = np.ascontiguousarray(uncond_attn, dtype=np.uint8)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        rows = cond_seq + uncond_seq
+        CV = self.cfg.n_codebooks * self.cfg.audio_vocab
+        out = np.empty((rows, CV), np.float32) if host_logits else None
+        _check(load().ovh_lm_forward_cfg(self.handle, cond_seq, uncond_seq, ids.ctypes.data,
+                                         am.ctypes.data, ca.ctypes.data, ua.ctypes.data,
+                                         pos.ctypes.data,
+                                         None if out is None else out.ctypes.data))
+        return out
+
+    def last_logits_ptr(self) -> int:
+        return load().ovh_lm_last_logits(self.handle) or 0
+
+    def set_device_sampling(self, on: bool) -> None:
+        load().ovh_lm_set_device_sampling(self.handle, int(bool(on)))
+
+    def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
+               target_len: int, guidance: float, layer_penalty: float):
+        import numpy as np
+        n = self.cfg.n_codebooks * target_len
+        pred = np.empty(n, np.int32)
+        scores = np.empty(n, np.float32)
+        _check(load().ovh_lm_sample(self.handle, C.c_void_p(cond_ptr), cond_seq,
+                                    C.c_void_p(uncond_ptr), uncond_seq, target_len, guidance,
+                                    layer_penalty, pred.ctypes.data, scores.ctypes.data))
+        return pred.reshape(self.cfg.n_codebooks, target_len), \
+            scores.reshape(self.cfg.n_codebooks, target_len)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            load().ovh_lm_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -14,8 +14,11 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libovnative_amd.so")
-SOURCES = ["quant.hip", "gemm.hip", "attn.hip", "capi.hip"]
+SOURCES = ["quant.hip", "gemm.hip", "attn.hip", "capi.hip", "lm.hip"]
+HOST_SOURCES = ["ovw1.cpp"]  # plain host C++ (no device code)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wextra"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -47,6 +50,13 @@ def build(verbose: bool = False) -> str:
             print(" ".join(cmd), flush=True)
         procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT), src))
         objs.append(obj)
+    for src in HOST_SOURCES:
+        obj = os.path.join(build_dir, src.replace(".cpp", ".o"))
+        cmd = [CXX, *HOST_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT), src))
+        objs.append(obj)
     failed = []
     for p, src in procs:
         out = p.communicate()[0].decode(errors="replace")
@@ -56,7 +66,7 @@ def build(verbose: bool = False) -> str:
         if p.returncode:
             failed.append(src)
     if failed:
-        raise RuntimeError(f"hipcc failed for {failed}")
+        raise RuntimeError(f"compile failed for {failed}")
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     subprocess.run(cmd, check=True)

@@ -15,29 +15,30 @@
 #include "gemm.h"
 #include "ovh_common.h"
 #include "quant.h"
+#include "status.h"
 
 struct OvhWeight {
   ovh::DeviceWeight w;
 };
 
 namespace {
-
 thread_local std::string t_err;
+}  // namespace
 
-int fail(int code, const std::string& msg) {
+namespace ovh {
+int set_error(int code, const std::string& msg) {
   t_err = msg;
   return code;
 }
-
-int hip_fail(hipError_t e, const char* what) {
-  return fail(OV_ERR_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
+int hip_error(hipError_t e, const char* what) {
+  return set_error(OV_ERR_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
 }
+}  // namespace ovh
 
-#define OVH_HIP(expr, what)                      \
-  do {                                           \
-    const hipError_t e_ = (expr);                \
-    if (e_ != hipSuccess) return hip_fail(e_, what); \
-  } while (0)
+namespace {
+
+int fail(int code, const std::string& msg) { return ovh::set_error(code, msg); }
+int hip_fail(hipError_t e, const char* what) { return ovh::hip_error(e, what); }
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -1,0 +1,736 @@
+// Device-resident LM runner for gfx950: the accelerator plugin of the reference
+// LM (cpp/src/backend/cuda/cuda_lm.h:26-57) rebuilt on the int8-nk HIP
+// operators.  Host code is plain C++17 around HIP; the numerics of every step
+// are those of the reference's CPU int8-nk forward (cpp/src/model/lm.cpp:217-401):
+//
+//   x = embed(ids)                                         lm.cpp:180-198
+//   per layer (lm.cpp:217-322):
+//     aq = rmsnorm_quantize(x, input_ln)                   one activation quantisation
+//     q|k|v = linear_q_sliced(aq, qkv)                     merged q/k/v weight
+//     q, k = qk_norm_rope(q, k)                            per-head RMSNorm + RoPE
+//     a = attention(q, k, v, bias)                         GQA, fp32
+//     x += linear(a, o)                                    quantise a, residual add
+//     aq = rmsnorm_quantize(x, post_ln)
+//     g|u = linear_q_sliced(aq, gate_up)
+//     x += linear_q(silu_mul_quantize(g, u), down)
+//   logits = linear(rmsnorm(x, final_norm), audio_heads)   lm.cpp:383-385
+//
+// The final norm and the head's activation quantisation are one fused kernel
+// (rmsnorm_quantize is byte-identical to rmsnorm followed by s8_nk_quantize).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ovnative_amd.h"
+#include "ovh_common.h"
+#include "status.h"
+
+namespace ovh {
+
+// ---------------------------------------------------------------------------
+// Embedding (lm.cpp:180-198, Emb::gather mat.cpp:57-67): a row with its audio
+// mask set is the sum, from 0 in codebook order, of audio_emb[ids[b,c,s] +
+// offsets[c]]; any other row is token_emb[ids[b,0,s]].  Tables are fp32, or
+// int8 with one scale per row gathered as float(q) * scale.  Ids were range-
+// checked on the host.
+struct EmbTable {
+  const float* f32;
+  const int8_t* i8;
+  const float* scale;
+};
+
+__device__ __forceinline__ float emb_at(const EmbTable& t, int64_t id, int64_t H, int64_t h) {
+  return t.f32 ? t.f32[id * H + h] : __fmul_rn((float)t.i8[id * H + h], t.scale[id]);
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
+                                                    const uint8_t* __restrict__ mask, int seq,
+                                                    int C, int64_t H, EmbTable tok, EmbTable aud,
+                                                    const int64_t* __restrict__ offsets,
+                                                    float* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / seq, s = row - b * seq;
+  float* o = out + row * H;
+  if (mask[row]) {
+    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
+      float acc = 0.f;
+      for (int c = 0; c < C; ++c) {
+        const int64_t id = ids[(b * C + c) * seq + s] + offsets[c];
+        acc = __fadd_rn(acc, emb_at(aud, id, H, h));
+      }
+      o[h] = acc;
+    }
+  } else {
+    const int64_t id = ids[b * C * seq + s];
+    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) o[h] = emb_at(tok, id, H, h);
+  }
+}
+
+// bias = attn ? 0 : -1e30 (lm.cpp:367).
+__global__ __launch_bounds__(256) void mask_to_bias_kernel(const uint8_t* __restrict__ m,
+                                                           float* __restrict__ bias, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) bias[i] = m[i] ? 0.f : -1e30f;
+}
+
+// ---------------------------------------------------------------------------
+// Guided sampling for one (codebook c, target frame t) per workgroup, the
+// per-step pass of cpp/src/model/tts.cpp:296-326 (device form as in
+// cuda_lm.cu:679-758): log_softmax of the conditional and unconditional
+// logits, lp = lc + g * (lc - lu) renormalised by a second log_softmax (when
+// g != 0), the mask token excluded, argmax (lowest index on ties) and
+// score = max - c * layer_penalty.  Both planes are token-major [S, C*V]: cond
+// at its last target_len positions, uncond at its first target_len positions.
+constexpr int kSampleThreads = 256;
+constexpr int kSampleMaxPer = 8;  // vocab <= 2048
+
+struct ArgMax {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ ArgMax better(ArgMax a, ArgMax b) {
+  return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+}
+
+__device__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kSampleThreads / 64; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__device__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kSampleThreads / 64; ++i) r = __fadd_rn(r, red[i]);
+  return r;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void guided_sample_kernel(
+    const float* __restrict__ cond, int cond_seq, const float* __restrict__ uncond, int C, int V,
+    int target_len, float guidance, float layer_penalty, int mask_id, int32_t* __restrict__ pred,
+    float* __restrict__ scores) {
+  __shared__ float red[kSampleThreads / 64];
+  __shared__ ArgMax ared[kSampleThreads / 64];
+  const int idx = blockIdx.x;
+  const int c = idx / target_len, t = idx - c * target_len;
+  const int64_t CV = (int64_t)C * V;
+  const float* lc = cond + (int64_t)(cond_seq - target_len + t) * CV + (int64_t)c * V;
+  const float* lu = uncond + (int64_t)t * CV + (int64_t)c * V;
+
+  float xc[kSampleMaxPer], xu[kSampleMaxPer];
+  float mc = -INFINITY, mu = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kSampleMaxPer; ++i) {
+    const int j = threadIdx.x + i * kSampleThreads;
+    xc[i] = j < V ? lc[j] : -INFINITY;
+    xu[i] = j < V ? lu[j] : -INFINITY;
+    mc = fmaxf(mc, xc[i]);
+    mu = fmaxf(mu, xu[i]);
+  }
+  mc = block_max(mc, red);
+  mu = block_max(mu, red);
+  float sc = 0.f, su = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSampleMaxPer; ++i) {
+    const int j = threadIdx.x + i * kSampleThreads;
+    if (j < V) {
+      sc = __fadd_rn(sc, expf(__fsub_rn(xc[i], mc)));
+      su = __fadd_rn(su, expf(__fsub_rn(xu[i], mu)));
+    }
+  }
+  sc = block_sum(sc, red);
+  su = block_sum(su, red);
+  const float lse_c = __fadd_rn(logf(sc), mc), lse_u = __fadd_rn(logf(su), mu);
+
+  float lp[kSampleMaxPer];
+  float m2 = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kSampleMaxPer; ++i) {
+    const float pc = __fsub_rn(xc[i], lse_c);
+    const float pu = __fsub_rn(xu[i], lse_u);
+    // tts.cpp is built for baseline x86-64 (no FMA): product and sum round separately
+    lp[i] = guidance != 0.f ? __fadd_rn(pc, __fmul_rn(guidance, __fsub_rn(pc, pu))) : pc;
+    const int j = threadIdx.x + i * kSampleThreads;
+    if (j < V) m2 = fmaxf(m2, lp[i]);
+  }
+  float lse2 = 0.f;
+  if (guidance != 0.f) {
+    m2 = block_max(m2, red);
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSampleMaxPer; ++i) {
+      const int j = threadIdx.x + i * kSampleThreads;
+      if (j < V) s2 = __fadd_rn(s2, expf(__fsub_rn(lp[i], m2)));
+    }
+    s2 = block_sum(s2, red);
+    lse2 = __fadd_rn(logf(s2), m2);
+  }
+  ArgMax best{-INFINITY, 0x7fffffff};
+#pragma unroll
+  for (int i = 0; i < kSampleMaxPer; ++i) {
+    const int j = threadIdx.x + i * kSampleThreads;
+    if (j < V && j != mask_id) {
+      const float v = guidance != 0.f ? __fsub_rn(lp[i], lse2) : lp[i];
+      best = better(best, ArgMax{v, j});
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ArgMax other{__shfl_xor(best.v, o), __shfl_xor(best.i, o)};
+    best = better(best, other);
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) ared[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ArgMax r = ared[0];
+    for (int i = 1; i < kSampleThreads / 64; ++i) r = better(r, ared[i]);
+    // argmax over an all -inf row stays at index 0, as the reference's loop does
+    pred[idx] = r.i == 0x7fffffff ? 0 : r.i;
+    scores[idx] = __fsub_rn(r.v, __fmul_rn((float)c, layer_penalty));
+  }
+}
+
+}  // namespace ovh
+
+// ===========================================================================
+// The runner.
+struct OvhLm {
+  OvhLmConfig cfg{};
+  hipStream_t st = nullptr;
+  struct Layer {
+    OvhWeight* qkv = nullptr;
+    OvhWeight* o = nullptr;
+    OvhWeight* gate_up = nullptr;
+    OvhWeight* down = nullptr;
+    float* ln1 = nullptr;
+    float* ln2 = nullptr;
+    float* qn = nullptr;
+    float* kn = nullptr;
+  };
+  std::vector<Layer> layers;
+  OvhWeight* head = nullptr;
+  float* final_norm = nullptr;
+  ovh::EmbTable tok{}, aud{};
+  int64_t tok_rows = 0, aud_rows = 0;
+  std::vector<int64_t> offsets;
+  int64_t* d_offsets = nullptr;
+  std::vector<void*> allocs;
+  // forward workspace (grow-only)
+  char* arena = nullptr;
+  size_t arena_cap = 0;
+  float* logits = nullptr;
+  bool device_sampling = false;
+  std::vector<float> host_flat;
+  int32_t* d_pred = nullptr;
+  float* d_scores = nullptr;
+  int64_t sample_cap = 0;
+  // RoPE tables of the last position list (rebuilt only when it changes)
+  std::vector<int64_t> tab_pos;
+  std::vector<float> tab_host;
+  float* d_tab = nullptr;
+  size_t tab_cap = 0;
+
+  ~OvhLm() {
+    for (auto& L : layers) {
+      ovh_weight_free(L.qkv);
+      ovh_weight_free(L.o);
+      ovh_weight_free(L.gate_up);
+      ovh_weight_free(L.down);
+    }
+    ovh_weight_free(head);
+    for (void* p : allocs) (void)hipFree(p);
+    if (arena) (void)hipFree(arena);
+    if (d_pred) (void)hipFree(d_pred);
+    if (d_scores) (void)hipFree(d_scores);
+    if (d_tab) (void)hipFree(d_tab);
+  }
+};
+
+namespace {
+
+using ovh::set_error;
+
+struct TensorIndex {
+  std::unordered_map<std::string, const OvhTensorView*> by_name;
+  const OvhTensorView* find(const std::string& n) const {
+    auto it = by_name.find(n);
+    return it == by_name.end() ? nullptr : it->second;
+  }
+};
+
+int missing(const std::string& name) {
+  return set_error(OV_ERR_INVALID_ARG, "LM weights: tensor not found: '" + name + "'");
+}
+
+int upload_bytes(OvhLm& L, const void* src, size_t n, void** out) {
+  void* d = nullptr;
+  OVH_HIP(hipMalloc(&d, n ? n : 1), "hipMalloc(LM tensor)");
+  L.allocs.push_back(d);
+  if (n) OVH_HIP(hipMemcpyAsync(d, src, n, hipMemcpyHostToDevice, L.st), "upload LM tensor");
+  *out = d;
+  return OV_OK;
+}
+
+// fp32 vector of `expect` elements (make_norm, mat.cpp:130-139).
+int load_norm(OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t expect,
+              float** out) {
+  const OvhTensorView* t = ix.find(name);
+  if (!t) return missing(name);
+  int64_t n = 1;
+  for (int i = 0; i < t->ndim; ++i) n *= t->dims[i];
+  if (t->dtype != 0 || n != expect || !t->data)
+    return set_error(OV_ERR_INVALID_ARG, name + ": expected " + std::to_string(expect) +
+                                             " fp32 elements");
+  void* d = nullptr;
+  const int rc = upload_bytes(L, t->data, sizeof(float) * (size_t)n, &d);
+  *out = static_cast<float*>(d);
+  return rc;
+}
+
+// An int8 linear weight with per-output-channel scales, OVW1 layout 0 ([N,K],
+// "nk") or 1 ([K,N], "kn"): make_linear, mat.cpp:69-106.
+int load_linear(const OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t N,
+                int64_t K, OvhWeight** out) {
+  const OvhTensorView* t = ix.find(name);
+  if (!t) return missing(name);
+  if (t->ndim != 2) return set_error(OV_ERR_INVALID_ARG, name + ": expected a 2-D weight");
+  if (t->dtype != 1 || !t->quantized || !t->scales)
+    return set_error(OV_ERR_NOT_IMPLEMENTED,
+                     name + ": the HIP runner takes int8 weights with per-channel scales");
+  const int layout = t->transposed ? 1 : 0;
+  const int64_t n = layout ? t->dims[1] : t->dims[0], k = layout ? t->dims[0] : t->dims[1];
+  if (n != N || k != K || t->n_scales != N)
+    return set_error(OV_ERR_INVALID_ARG, name + ": shape mismatch (expected N=" +
+                                             std::to_string(N) + ", K=" + std::to_string(K) + ")");
+  return ovh_weight_upload(N, K, static_cast<const int8_t*>(t->data), t->scales, layout, L.st, out);
+}
+
+// Embedding table [rows, H]: fp32, or int8 + per-row scale (make_emb, mat.cpp:108-128).
+int load_emb(OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t H,
+             ovh::EmbTable* tab, int64_t* rows) {
+  const OvhTensorView* t = ix.find(name);
+  if (!t) return missing(name);
+  if (t->ndim != 2 || t->transposed || t->dims[1] != H)
+    return set_error(OV_ERR_INVALID_ARG, name + ": expected a row-major [rows, hidden] table");
+  *rows = t->dims[0];
+  void* d = nullptr;
+  *tab = ovh::EmbTable{nullptr, nullptr, nullptr};
+  if (t->dtype == 0) {
+    int rc = upload_bytes(L, t->data, sizeof(float) * (size_t)(t->dims[0] * H), &d);
+    tab->f32 = static_cast<const float*>(d);
+    return rc;
+  }
+  if (t->dtype == 1 && t->quantized && t->scales && t->n_scales == t->dims[0]) {
+    int rc = upload_bytes(L, t->data, (size_t)(t->dims[0] * H), &d);
+    if (rc != OV_OK) return rc;
+    tab->i8 = static_cast<const int8_t*>(d);
+    rc = upload_bytes(L, t->scales, sizeof(float) * (size_t)t->dims[0], &d);
+    tab->scale = static_cast<const float*>(d);
+    return rc;
+  }
+  return set_error(OV_ERR_INVALID_ARG, name + ": unsupported dtype for an embedding");
+}
+
+int build(OvhLm& L, const TensorIndex& ix) {
+  const OvhLmConfig& c = L.cfg;
+  const int64_t H = c.hidden, QD = (int64_t)c.n_heads * c.head_dim,
+                KVD = (int64_t)c.n_kv_heads * c.head_dim, I = c.inter;
+  int rc = load_emb(L, ix, "llm.embed_tokens.weight", H, &L.tok, &L.tok_rows);
+  if (rc == OV_OK) rc = load_emb(L, ix, "audio_embeddings.weight", H, &L.aud, &L.aud_rows);
+  if (rc != OV_OK) return rc;
+  if (L.aud_rows != (int64_t)c.n_codebooks * c.audio_vocab)
+    return set_error(OV_ERR_INVALID_ARG, "audio embedding rows mismatch");
+  rc = load_linear(L, ix, "audio_heads.weight", (int64_t)c.n_codebooks * c.audio_vocab, H, &L.head);
+  if (rc == OV_OK) rc = load_norm(L, ix, "llm.norm.weight", H, &L.final_norm);
+  if (rc != OV_OK) return rc;
+  const OvhTensorView* offs = ix.find("codebook_layer_offsets");
+  if (!offs) return missing("codebook_layer_offsets");
+  if (offs->dtype != 3 || offs->ndim < 1 || offs->dims[0] != c.n_codebooks || !offs->data)
+    return set_error(OV_ERR_INVALID_ARG, "codebook_layer_offsets: unexpected size");
+  L.offsets.assign(static_cast<const int64_t*>(offs->data),
+                   static_cast<const int64_t*>(offs->data) + c.n_codebooks);
+  void* d = nullptr;
+  rc = upload_bytes(L, L.offsets.data(), sizeof(int64_t) * L.offsets.size(), &d);
+  if (rc != OV_OK) return rc;
+  L.d_offsets = static_cast<int64_t*>(d);
+
+  L.layers.resize((size_t)c.n_layers);
+  for (int i = 0; i < c.n_layers; ++i) {
+    const std::string p = "llm.layers." + std::to_string(i) + ".";
+    OvhLm::Layer& Y = L.layers[(size_t)i];
+    rc = load_norm(L, ix, p + "input_layernorm.weight", H, &Y.ln1);
+    if (rc == OV_OK) rc = load_norm(L, ix, p + "post_attention_layernorm.weight", H, &Y.ln2);
+    if (rc == OV_OK) rc = load_norm(L, ix, p + "self_attn.q_norm.weight", c.head_dim, &Y.qn);
+    if (rc == OV_OK) rc = load_norm(L, ix, p + "self_attn.k_norm.weight", c.head_dim, &Y.kn);
+    OvhWeight *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *u = nullptr;
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "self_attn.q_proj.weight", QD, H, &q);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "self_attn.k_proj.weight", KVD, H, &k);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "self_attn.v_proj.weight", KVD, H, &v);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "self_attn.o_proj.weight", H, QD, &Y.o);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "mlp.gate_proj.weight", I, H, &g);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "mlp.up_proj.weight", I, H, &u);
+    if (rc == OV_OK) rc = load_linear(L, ix, p + "mlp.down_proj.weight", H, I, &Y.down);
+    // q/k/v and gate/up merged once at load time (combine_packed, lm.cpp:57-94).
+    if (rc == OV_OK) {
+      const OvhWeight* parts[3] = {q, k, v};
+      rc = ovh_weight_concat(parts, 3, L.st, &Y.qkv);
+    }
+    if (rc == OV_OK) {
+      const OvhWeight* parts[2] = {g, u};
+      rc = ovh_weight_concat(parts, 2, L.st, &Y.gate_up);
+    }
+    ovh_weight_free(q);
+    ovh_weight_free(k);
+    ovh_weight_free(v);
+    ovh_weight_free(g);
+    ovh_weight_free(u);
+    if (rc != OV_OK) return rc;
+  }
+  OVH_HIP(hipStreamSynchronize(L.st), "LM upload");
+  return OV_OK;
+}
+
+// One attention segment as given by the caller (host mask, nullable).
+struct SegIn {
+  const uint8_t* mask;  // [rows, rows], 1 = attend; nullptr = all attend
+  int rows;
+  int64_t row0;
+};
+
+// RoPE cos/sin tables [T, D/2] for the position list, built on the host exactly
+// as qk_norm_rope_f32 builds its cached tables (cpp/src/backend/cpu/ops_cpu.cpp:
+// 958-993): inv_freq = (float)pow(theta, -2i/D) in double, angle = (float)pos *
+// inv_freq in float, then libm cosf / sinf, so the tables are the reference's
+// bits.  Like the reference, the tables are cached by position list: a decode
+// loop whose positions do not change builds and uploads them once.
+int rope_tables_cached(OvhLm& L, const int64_t* pos, int64_t T, float** cos_out,
+                       float** sin_out) {
+  const int D = L.cfg.head_dim, half = D / 2;
+  const size_t n = (size_t)T * half;
+  const bool same = (int64_t)L.tab_pos.size() == T &&
+                    std::equal(L.tab_pos.begin(), L.tab_pos.end(), pos);
+  if (!same) {
+    if (2 * n > L.tab_cap) {
+      if (L.d_tab) OVH_HIP(hipFree(L.d_tab), "hipFree(rope tables)");
+      L.d_tab = nullptr;
+      L.tab_cap = 0;
+      OVH_HIP(hipMalloc(reinterpret_cast<void**>(&L.d_tab), sizeof(float) * 2 * n),
+              "hipMalloc(rope tables)");
+      L.tab_cap = 2 * n;
+    }
+    std::vector<float> inv_freq((size_t)half);
+    for (int i = 0; i < half; ++i)
+      inv_freq[(size_t)i] = (float)std::pow((double)L.cfg.rope_theta, -2.0 * i / (double)D);
+    L.tab_host.resize(2 * n);
+    for (int64_t r = 0; r < T; ++r) {
+      const float p = (float)pos[r];
+      for (int i = 0; i < half; ++i) {
+        const float angle = p * inv_freq[(size_t)i];
+        L.tab_host[(size_t)r * half + i] = std::cos(angle);
+        L.tab_host[n + (size_t)r * half + i] = std::sin(angle);
+      }
+    }
+    OVH_HIP(hipMemcpyAsync(L.d_tab, L.tab_host.data(), sizeof(float) * 2 * n,
+                           hipMemcpyHostToDevice, L.st),
+            "upload rope tables");
+    L.tab_pos.assign(pos, pos + T);
+  }
+  *cos_out = L.d_tab;
+  *sin_out = L.d_tab + n;
+  return OV_OK;
+}
+
+bool all_ones(const uint8_t* m, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    if (!m[i]) return false;
+  return true;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Forward over T rows laid out as `batch` x `seq` for the embedding's id indexing
+// ([batch, C, seq]), attention split into `segs`.
+int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
+                 const int64_t* ids, const uint8_t* audio_mask, const int64_t* pos) {
+  const OvhLmConfig& c = L.cfg;
+  const int64_t T = (int64_t)batch * seq;
+  const int64_t H = c.hidden, D = c.head_dim, QD = (int64_t)c.n_heads * D,
+                KVD = (int64_t)c.n_kv_heads * D, I = c.inter, C = c.n_codebooks,
+                CV = (int64_t)c.n_codebooks * c.audio_vocab, half = D / 2;
+  // Id range checks (Emb::gather throws on these, mat.cpp:58-60).
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t s = 0; s < seq; ++s) {
+      const int64_t row = b * seq + s;
+      if (audio_mask[row]) {
+        for (int64_t cb = 0; cb < C; ++cb) {
+          const int64_t id = ids[(b * C + cb) * seq + s] + L.offsets[(size_t)cb];
+          if (id < 0 || id >= L.aud_rows)
+            return set_error(OV_ERR_INVALID_ARG, "embedding id out of range: " + std::to_string(id));
+        }
+      } else {
+        const int64_t id = ids[b * C * seq + s];
+        if (id < 0 || id >= L.tok_rows)
+          return set_error(OV_ERR_INVALID_ARG, "embedding id out of range: " + std::to_string(id));
+      }
+    }
+  // Masks that are all ones add a zero bias: skip them.
+  std::vector<int64_t> bias_off(segs.size(), -1);
+  int64_t bias_elems = 0;
+  for (size_t i = 0; i < segs.size(); ++i) {
+    const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
+    if (segs[i].mask && !all_ones(segs[i].mask, n)) {
+      bias_off[i] = bias_elems;
+      bias_elems += n;
+    }
+  }
+  const int64_t Kp_max = 32 * ovh::kb_of(I > QD ? (I > H ? I : H) : (QD > H ? QD : H));
+  const int64_t Kb_max = Kp_max / 32;
+  struct Buf {
+    size_t off, bytes;
+  };
+  size_t cur = 0;
+  auto take = [&](size_t bytes) {
+    Buf b{cur, bytes};
+    cur = align256(cur + bytes);
+    return b;
+  };
+  const Buf b_ids = take(sizeof(int64_t) * (size_t)(T * C)), b_am = take((size_t)T),
+            b_mask = take((size_t)bias_elems), b_bias = take(sizeof(float) * (size_t)bias_elems),
+            b_x = take(sizeof(float) * (size_t)(T * H)),
+            b_aq = take((size_t)(T * Kp_max)), b_asc = take(sizeof(float) * (size_t)(T * Kb_max)),
+            b_q = take(sizeof(float) * (size_t)(T * QD)), b_k = take(sizeof(float) * (size_t)(T * KVD)),
+            b_v = take(sizeof(float) * (size_t)(T * KVD)), b_at = take(sizeof(float) * (size_t)(T * QD)),
+            b_g = take(sizeof(float) * (size_t)(T * I)), b_u = take(sizeof(float) * (size_t)(T * I)),
+            b_lg = take(sizeof(float) * (size_t)(T * CV));
+  if (cur > L.arena_cap) {
+    if (L.arena) OVH_HIP(hipFree(L.arena), "hipFree(arena)");
+    L.arena = nullptr;
+    L.arena_cap = 0;
+    const size_t want = cur + cur / 4 + ((size_t)1 << 20);
+    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&L.arena), want), "hipMalloc(arena)");
+    L.arena_cap = want;
+  }
+  auto at = [&](const Buf& b) { return static_cast<void*>(L.arena + b.off); };
+  int64_t* d_ids = static_cast<int64_t*>(at(b_ids));
+  uint8_t* d_am = static_cast<uint8_t*>(at(b_am));
+  float* x = static_cast<float*>(at(b_x));
+  int8_t* aq = static_cast<int8_t*>(at(b_aq));
+  float* asc = static_cast<float*>(at(b_asc));
+  float* q = static_cast<float*>(at(b_q));
+  float* k = static_cast<float*>(at(b_k));
+  float* v = static_cast<float*>(at(b_v));
+  float* att = static_cast<float*>(at(b_at));
+  float* gate = static_cast<float*>(at(b_g));
+  float* up = static_cast<float*>(at(b_u));
+  float* logits = static_cast<float*>(at(b_lg));
+  hipStream_t st = L.st;
+
+  OVH_HIP(hipMemcpyAsync(d_ids, ids, b_ids.bytes, hipMemcpyHostToDevice, st), "upload ids");
+  OVH_HIP(hipMemcpyAsync(d_am, audio_mask, b_am.bytes, hipMemcpyHostToDevice, st), "upload mask");
+  std::vector<OvhAttnSegment> asegs(segs.size());
+  for (size_t i = 0; i < segs.size(); ++i) {
+    const float* bias = nullptr;
+    if (bias_off[i] >= 0) {
+      const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
+      uint8_t* m = static_cast<uint8_t*>(at(b_mask)) + bias_off[i];
+      float* bb = static_cast<float*>(at(b_bias)) + bias_off[i];
+      OVH_HIP(hipMemcpyAsync(m, segs[i].mask, (size_t)n, hipMemcpyHostToDevice, st), "upload attn mask");
+      hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         st, m, bb, n);
+      OVH_HIP(hipGetLastError(), "mask_to_bias launch");
+      bias = bb;
+    }
+    asegs[i] = OvhAttnSegment{bias, segs[i].rows, segs[i].row0 * QD, segs[i].row0 * KVD};
+  }
+  float *cosb = nullptr, *sinb = nullptr;
+  int rc = rope_tables_cached(L, pos, T, &cosb, &sinb);
+  if (rc != OV_OK) return rc;
+  hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)T), dim3(256), 0, st, d_ids, d_am, seq,
+                     (int)C, H, L.tok, L.aud, L.d_offsets, x);
+  OVH_HIP(hipGetLastError(), "embed launch");
+
+  const float scale = 1.f / std::sqrt((float)D);
+  const int64_t qkv_n[3] = {QD, KVD, KVD};
+  float* qkv_c[3] = {q, k, v};
+  const int64_t gu_n[2] = {I, I};
+  float* gu_c[2] = {gate, up};
+  for (const OvhLm::Layer& Y : L.layers) {
+    if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln1, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+    if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st)) != OV_OK) return rc;
+    if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb, sinb,
+                               c.rms_eps, st)) != OV_OK)
+      return rc;
+    if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
+                            QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
+      return rc;
+    if ((rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
+    if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
+    if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+    if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
+    if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
+    if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+  }
+  if ((rc = ovh_rmsnorm_quantize(T, H, x, L.final_norm, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+  if ((rc = ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st)) != OV_OK) return rc;
+  L.logits = logits;
+  return OV_OK;
+}
+
+bool config_ok(const OvhLmConfig& c) {
+  return c.n_layers > 0 && c.hidden > 0 && c.n_heads > 0 && c.n_kv_heads > 0 &&
+         c.n_heads % c.n_kv_heads == 0 && c.head_dim == 128 && c.inter > 0 &&
+         c.audio_vocab > 1 && c.audio_vocab <= ovh::kSampleThreads * ovh::kSampleMaxPer &&
+         c.n_codebooks > 0 && c.hidden % 64 == 0 && ((int64_t)c.n_heads * c.head_dim) % 64 == 0 &&
+         ((int64_t)c.n_kv_heads * c.head_dim) % 64 == 0 && c.inter % 64 == 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_tensors,
+                  void* stream, OvhLm** out) {
+  if (!out) return set_error(OV_ERR_INVALID_ARG, "out is null");
+  *out = nullptr;
+  if (!cfg || !tensors || n_tensors <= 0) return set_error(OV_ERR_INVALID_ARG, "no config/tensors");
+  if (!config_ok(*cfg))
+    return set_error(OV_ERR_NOT_IMPLEMENTED,
+                     "LM config: the HIP runner needs head_dim 128, n_heads % n_kv_heads == 0, "
+                     "projection widths that are multiples of 64 and audio_vocab <= 2048");
+  TensorIndex ix;
+  for (int i = 0; i < n_tensors; ++i)
+    if (tensors[i].name) ix.by_name[tensors[i].name] = &tensors[i];
+  OvhLm* L = new (std::nothrow) OvhLm();
+  if (!L) return set_error(OV_ERR_INTERNAL, "out of host memory");
+  L->cfg = *cfg;
+  L->st = static_cast<hipStream_t>(stream);
+  const int rc = build(*L, ix);
+  if (rc != OV_OK) {
+    (void)hipStreamSynchronize(L->st);
+    delete L;
+    return rc;
+  }
+  *out = L;
+  return OV_OK;
+}
+
+void ovh_lm_destroy(OvhLm* lm) {
+  if (!lm) return;
+  (void)hipStreamSynchronize(lm->st);
+  delete lm;
+}
+
+int ovh_lm_forward(OvhLm* lm, int batch, int seq, const int64_t* input_ids,
+                   const uint8_t* audio_mask, const uint8_t* attn_mask,
+                   const int64_t* position_ids, float* logits) {
+  if (!lm) return set_error(OV_ERR_INVALID_ARG, "lm is null");
+  if (batch <= 0 || seq <= 0) return set_error(OV_ERR_INVALID_ARG, "batch and seq must be positive");
+  if (!input_ids || !audio_mask || !attn_mask || !position_ids)
+    return set_error(OV_ERR_INVALID_ARG, "null host input");
+  std::vector<SegIn> segs((size_t)batch);
+  for (int b = 0; b < batch; ++b)
+    segs[(size_t)b] = SegIn{attn_mask + (int64_t)b * seq * seq, seq, (int64_t)b * seq};
+  int rc = forward_rows(*lm, batch, seq, segs, input_ids, audio_mask, position_ids);
+  if (rc != OV_OK) return rc;
+  if (!logits || lm->device_sampling) return OV_OK;
+  // [B*S, C*V] on the device -> [B, C, S, V] on the host (cuda_lm.cu:1184-1199).
+  const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab;
+  const size_t n = (size_t)batch * seq * C * V;
+  lm->host_flat.resize(n);
+  OVH_HIP(hipMemcpyAsync(lm->host_flat.data(), lm->logits, sizeof(float) * n,
+                         hipMemcpyDeviceToHost, lm->st),
+          "download logits");
+  OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
+  for (int b = 0; b < batch; ++b)
+    for (int cb = 0; cb < C; ++cb)
+      for (int s = 0; s < seq; ++s)
+        std::memcpy(logits + (((size_t)b * C + cb) * seq + s) * V,
+                    lm->host_flat.data() + ((size_t)b * seq + s) * C * V + (size_t)cb * V,
+                    sizeof(float) * (size_t)V);
+  return OV_OK;
+}
+
+int ovh_lm_forward_cfg(OvhLm* lm, int cond_seq, int uncond_seq, const int64_t* input_ids,
+                       const uint8_t* audio_mask, const uint8_t* cond_attn,
+                       const uint8_t* uncond_attn, const int64_t* position_ids, float* logits) {
+  if (!lm) return set_error(OV_ERR_INVALID_ARG, "lm is null");
+  if (cond_seq <= 0 || uncond_seq <= 0)
+    return set_error(OV_ERR_INVALID_ARG, "forward_cfg: both segments must be non-empty");
+  if (!input_ids || !audio_mask || !cond_attn || !uncond_attn || !position_ids)
+    return set_error(OV_ERR_INVALID_ARG, "null host input");
+  const int rows = cond_seq + uncond_seq;
+  std::vector<SegIn> segs = {SegIn{cond_attn, cond_seq, 0}, SegIn{uncond_attn, uncond_seq, cond_seq}};
+  int rc = forward_rows(*lm, 1, rows, segs, input_ids, audio_mask, position_ids);
+  if (rc != OV_OK) return rc;
+  if (!logits || lm->device_sampling) return OV_OK;
+  const size_t n = (size_t)rows * lm->cfg.n_codebooks * lm->cfg.audio_vocab;
+  OVH_HIP(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n, hipMemcpyDeviceToHost, lm->st),
+          "download logits");
+  OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
+  return OV_OK;
+}
+
+const void* ovh_lm_last_logits(const OvhLm* lm) { return lm ? lm->logits : nullptr; }
+
+void ovh_lm_set_device_sampling(OvhLm* lm, int on) {
+  if (lm) lm->device_sampling = on != 0;
+}
+
+int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,
+                  int target_len, float guidance, float layer_penalty, int32_t* pred,
+                  float* scores) {
+  if (!lm) return set_error(OV_ERR_INVALID_ARG, "lm is null");
+  if (!cond || !uncond || !pred || !scores) return set_error(OV_ERR_INVALID_ARG, "null argument");
+  if (target_len <= 0 || target_len > cond_seq || target_len > uncond_seq)
+    return set_error(OV_ERR_INVALID_ARG, "sample: need 0 < target_len <= both plane lengths");
+  const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab;
+  const int64_t n = (int64_t)C * target_len;
+  if (n > lm->sample_cap) {
+    if (lm->d_pred) OVH_HIP(hipFree(lm->d_pred), "hipFree");
+    if (lm->d_scores) OVH_HIP(hipFree(lm->d_scores), "hipFree");
+    lm->d_pred = nullptr;
+    lm->d_scores = nullptr;
+    lm->sample_cap = 0;
+    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&lm->d_pred), sizeof(int32_t) * (size_t)n), "hipMalloc(pred)");
+    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&lm->d_scores), sizeof(float) * (size_t)n), "hipMalloc(scores)");
+    lm->sample_cap = n;
+  }
+  // The mask token is the last audio id (kMaskId = 1024 with audio_vocab 1025,
+  // cpp/src/model/tts.cpp:17).
+  hipLaunchKernelGGL(ovh::guided_sample_kernel, dim3((unsigned)n), dim3(ovh::kSampleThreads), 0,
+                     lm->st, static_cast<const float*>(cond), cond_seq,
+                     static_cast<const float*>(uncond), C, V, target_len, guidance, layer_penalty,
+                     V - 1, lm->d_pred, lm->d_scores);
+  OVH_HIP(hipGetLastError(), "guided sample launch");
+  OVH_HIP(hipMemcpyAsync(pred, lm->d_pred, sizeof(int32_t) * (size_t)n, hipMemcpyDeviceToHost, lm->st),
+          "download pred");
+  OVH_HIP(hipMemcpyAsync(scores, lm->d_scores, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost,
+                         lm->st),
+          "download scores");
+  OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
+  return OV_OK;
+}
+
+}  // extern "C"

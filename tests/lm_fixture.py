@@ -1,0 +1,82 @@
+"""Random LM checkpoints for the tests: the reference's tensor names and
+encodings (tools/convert_weights.py: int8 linears per output channel in the nk
+or kn layout, int8 embedding tables with per-row scales, fp32 norms), with
+weights ~N(0, 0.02) and norm weights near 1."""
+from __future__ import annotations
+
+import numpy as np
+
+from ovnative_amd import ovw1
+
+SMALL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, inter=512,
+             vocab=300, audio_vocab=33, n_codebooks=8, rms_eps=1e-6, rope_theta=1e6)
+
+
+def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True):
+    """Returns (tensors for ovw1.write / views, {name: (array, scales, transposed)})."""
+    rng = np.random.default_rng(seed)
+    H, NH, NKV, D, I = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["inter"]
+    Cb, V = cfg["n_codebooks"], cfg["audio_vocab"]
+    ts = []
+
+    def lin(name, n, k):
+        ts.append(ovw1.linear_int8(name, (rng.standard_normal((n, k)) * 0.02).astype(np.float32),
+                                   layout))
+
+    def norm(name, n):
+        ts.append(ovw1.Tensor(name, rng.uniform(0.8, 1.2, n).astype(np.float32)))
+
+    def emb(name, rows):
+        w = (rng.standard_normal((rows, H)) * 0.02).astype(np.float32)
+        if emb_int8:
+            q, s = ovw1.quantize_int8(w)
+            ts.append(ovw1.Tensor(name, q, 0, s))
+        else:
+            ts.append(ovw1.Tensor(name, w))
+
+    emb("llm.embed_tokens.weight", cfg["vocab"])
+    emb("audio_embeddings.weight", Cb * V)
+    lin("audio_heads.weight", Cb * V, H)
+    norm("llm.norm.weight", H)
+    ts.append(ovw1.Tensor("codebook_layer_offsets", np.arange(Cb, dtype=np.int64) * V))
+    for i in range(cfg["n_layers"]):
+        p = f"llm.layers.{i}."
+        norm(p + "input_layernorm.weight", H)
+        norm(p + "post_attention_layernorm.weight", H)
+        norm(p + "self_attn.q_norm.weight", D)
+        norm(p + "self_attn.k_norm.weight", D)
+        lin(p + "self_attn.q_proj.weight", NH * D, H)
+        lin(p + "self_attn.k_proj.weight", NKV * D, H)
+        lin(p + "self_attn.v_proj.weight", NKV * D, H)
+        lin(p + "self_attn.o_proj.weight", H, NH * D)
+        lin(p + "mlp.gate_proj.weight", I, H)
+        lin(p + "mlp.up_proj.weight", I, H)
+        lin(p + "mlp.down_proj.weight", H, I)
+    table = {t.name: (t.array, t.scales, t.layout == 1) for t in ts}
+    return ts, table
+
+
+def make_inputs(seed: int, cfg: dict, batch: int, seq: int, text: int):
+    """A CFG-style batch like tts.cpp:175-213 builds: `text` text positions then
+    audio positions in row 0; row 1 holds only the target audio (attends within
+    its first seq - text positions, diagonal for the tail)."""
+    rng = np.random.default_rng(seed)
+    Cb, V = cfg["n_codebooks"], cfg["audio_vocab"]
+    ids = rng.integers(0, V - 1, (batch, Cb, seq)).astype(np.int64)
+    ids[:, 0, :text] = rng.integers(0, cfg["vocab"], (batch, text))
+    amask = np.zeros((batch, seq), np.uint8)
+    amask[:, text:] = 1
+    attn = np.ones((batch, seq, seq), np.uint8)
+    if batch > 1:
+        # row 1: the target slice of row 0 in its first T positions, the mask
+        # token elsewhere (tts.cpp:190-198)
+        T = seq - text
+        ids[1] = V - 1
+        ids[1, :, :T] = ids[0, :, text:]
+        attn[1] = 0
+        attn[1, :T, :T] = 1
+        attn[1, np.arange(T, seq), np.arange(T, seq)] = 1
+        amask[1] = 0
+        amask[1, :T] = 1
+    pos = np.tile(np.arange(seq, dtype=np.int64), (batch, 1))
+    return ids, amask, attn, pos

@@ -163,3 +163,55 @@ def test_embed_brute_force(oracle):
         bad = ids.copy()
         bad[0, 0, :] = 10_000
         oracle.embed(bad, np.zeros_like(mask), tok, aud, offs)
+
+
+def _np_guided(cond, cond_seq, uncond, C, V, T, g, pen, mask_id):
+    """float64 statement of tts.cpp:296-326 (log_softmax, mix, mask, argmax)."""
+    def lsm(x):
+        m = x.max()
+        return x - (np.log(np.exp(x - m).sum()) + m)
+    pred = np.zeros((C, T), np.int64)
+    score = np.zeros((C, T))
+    gap = np.zeros((C, T))
+    for c in range(C):
+        for t in range(T):
+            lc = lsm(cond[cond_seq - T + t, c * V:(c + 1) * V].astype(np.float64))
+            lu = lsm(uncond[t, c * V:(c + 1) * V].astype(np.float64))
+            mix = lsm(lc + g * (lc - lu)) if g != 0 else lc
+            mix[mask_id] = -np.inf
+            srt = np.sort(mix)
+            pred[c, t], score[c, t], gap[c, t] = mix.argmax(), srt[-1] - c * pen, srt[-1] - srt[-2]
+    return pred, score, gap
+
+
+@pytest.mark.parametrize("g", [0.0, 2.0])
+def test_guided_sample_properties(oracle, g):
+    rng = np.random.default_rng(int(g * 10) + 1)
+    C, V, S, T = 8, 1025, 12, 7
+    cond = (rng.standard_normal((S, C * V)) * 3).astype(np.float32)
+    uncond = (rng.standard_normal((T, C * V)) * 3).astype(np.float32)
+    cond[S - T, 1024] = 100.0          # the mask token never wins
+    pred, score = oracle.guided_sample(cond, S, uncond, C, V, T, g, 5.0)
+    want, wscore, gap = _np_guided(cond, S, uncond, C, V, T, g, 5.0, 1024)
+    clear = gap > 1e-4
+    assert np.array_equal(pred[clear], want[clear]) and np.all(pred != 1024)
+    np.testing.assert_allclose(score, wscore, rtol=0, atol=2e-5)
+
+
+def test_guided_sample_host_alias_quirk(oracle):
+    """tts.cpp's host path renormalises lp_mix with log_softmax(x, n, x) in place,
+    so its guided values are exp(mix - m) - lse (the function's last loop reads
+    the overwritten x).  Same argmax as the device form wherever exp() does not
+    underflow; scores are 1 - lse instead of max(mix) - lse."""
+    rng = np.random.default_rng(21)
+    C, V, S, T = 8, 1025, 6, 4
+    cond = rng.standard_normal((S, C * V)).astype(np.float32)
+    uncond = rng.standard_normal((T, C * V)).astype(np.float32)
+    p_dev, s_dev = oracle.guided_sample(cond, S, uncond, C, V, T, 2.0, 5.0)
+    p_cpu, s_cpu = oracle.guided_sample(cond, S, uncond, C, V, T, 2.0, 5.0, cpu_alias=True)
+    assert np.array_equal(p_dev, p_cpu)
+    # host score = exp(mix_best - m) - lse - c*pen with mix_best = m: 1 - lse - c*pen,
+    # device score = m - lse - c*pen, so host - device = 1 - m  (m = max mix)
+    want, _, _ = _np_guided(cond, S, uncond, C, V, T, 2.0, 5.0, 1024)
+    assert np.array_equal(p_dev, want)
+    assert not np.allclose(s_dev, s_cpu)
