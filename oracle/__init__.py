@@ -385,6 +385,11 @@ class Reference:
             "ovref_ovw1_close": (None, [_p]),
             "ovref_ovw1_count": (C.c_int, [_p]),
             "ovref_ovw1_get": (C.c_int, [_p, C.c_char_p] + [_p] * 11),
+            "ovref_lm_open": (_p, [C.c_char_p] + [C.c_int] * 9 + [_f32, _f32, C.c_char_p,
+                                                                  C.c_size_t]),
+            "ovref_lm_close": (None, [_p]),
+            "ovref_lm_forward": (C.c_int, [_p, C.c_int, C.c_int, _p, _p, _p, _p, _p]),
+            "ovref_lm_forward_cfg": (C.c_int, [_p, C.c_int, C.c_int, _p, _p, _p, _p, _p, _p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -393,6 +398,33 @@ class Reference:
 
     def vnni_available(self) -> bool:
         return bool(self.lib.ovref_vnni_available())
+
+    def lm_open(self, path, cfg):
+        """The reference LM (lm.cpp) on an OVW1 checkpoint; cfg = LMConfig fields."""
+        err = C.create_string_buffer(512)
+        keys = ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "inter", "vocab",
+                "audio_vocab", "n_codebooks")
+        h = self.lib.ovref_lm_open(os.fsencode(path), *[int(cfg[k]) for k in keys],
+                                   float(cfg.get("rms_eps", 1e-6)),
+                                   float(cfg.get("rope_theta", 1e6)), err, 512)
+        if not h:
+            raise RuntimeError(err.value.decode())
+        return h
+
+    def lm_close(self, h):
+        self.lib.ovref_lm_close(h)
+
+    def lm_forward(self, h, cfg, ids, audio_mask, attn_mask, pos):
+        """LM::forward: returns logits [B, C, S, V]."""
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        am = np.ascontiguousarray(audio_mask, dtype=np.uint8)
+        at = np.ascontiguousarray(attn_mask, dtype=np.uint8)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        B, Cb, S = ids.shape
+        out = np.empty((B, Cb, S, int(cfg["audio_vocab"])), np.float32)
+        if self.lib.ovref_lm_forward(h, B, S, _ptr(ids), _ptr(am), _ptr(at), _ptr(pos), _ptr(out)):
+            raise RuntimeError("reference LM::forward failed")
+        return out
 
     def ovw1_read(self, path, names):
         """Open `path` with the reference loader (WeightFile::Open); returns

@@ -10,6 +10,7 @@
 #include <stdexcept>
 #include <vector>
 
+#include "model/lm.h"
 #include "model/ops.h"
 #include "ovnative/ov_gemm.h"
 #include "ovnative/ov_weights.h"
@@ -124,4 +125,44 @@ REF_API int ovref_ovw1_get(void* h, const char* name, int* dtype, int* ndim, int
   *stored_crc = wf->StoredCrc(*t);
   *computed_crc = wf->ComputeCrc(*t);
   return 0;
+}
+
+// The reference LM (cpp/src/model/lm.cpp) over an OVW1 file: LM::forward and
+// LM::forward_cfg on the host, for the LM parity pin and the CPU baseline.
+struct RefLm {
+  ov::WeightFile wf;
+  ov::LM lm;
+  RefLm(ov::WeightFile&& w, const ov::LMConfig& c) : wf(std::move(w)), lm(wf, c) {}
+};
+REF_API void* ovref_lm_open(const char* path, int n_layers, int hidden, int n_heads,
+                            int n_kv_heads, int head_dim, int inter, int vocab, int audio_vocab,
+                            int n_codebooks, float rms_eps, float rope_theta, char* err,
+                            size_t n) {
+  try {
+    ov::LMConfig c;
+    c.n_layers = n_layers; c.hidden = hidden; c.n_heads = n_heads; c.n_kv_heads = n_kv_heads;
+    c.head_dim = head_dim; c.inter = inter; c.vocab = vocab; c.audio_vocab = audio_vocab;
+    c.n_codebooks = n_codebooks; c.rms_eps = rms_eps; c.rope_theta = rope_theta;
+    return new RefLm(ov::WeightFile::Open(path), c);
+  } catch (const std::exception& e) {
+    if (err && n) std::snprintf(err, n, "%s", e.what());
+    return nullptr;
+  }
+}
+REF_API void ovref_lm_close(void* h) { delete static_cast<RefLm*>(h); }
+REF_API int ovref_lm_forward(void* h, int batch, int seq, const int64_t* ids, const uint8_t* amask,
+                             const uint8_t* attn, const int64_t* pos, float* logits) {
+  try {
+    static_cast<RefLm*>(h)->lm.forward(batch, seq, ids, amask, attn, pos, logits);
+    return 0;
+  } catch (const std::exception&) { return -1; }
+}
+REF_API int ovref_lm_forward_cfg(void* h, int cond_seq, int uncond_seq, const int64_t* ids,
+                                 const uint8_t* amask, const uint8_t* cond_attn,
+                                 const uint8_t* uncond_attn, const int64_t* pos, float* logits) {
+  try {
+    static_cast<RefLm*>(h)->lm.forward_cfg(cond_seq, uncond_seq, ids, amask, cond_attn,
+                                           uncond_attn, pos, logits);
+    return 0;
+  } catch (const std::exception&) { return -1; }
 }

@@ -215,3 +215,37 @@ def test_guided_sample_host_alias_quirk(oracle):
     want, _, _ = _np_guided(cond, S, uncond, C, V, T, 2.0, 5.0, 1024)
     assert np.array_equal(p_dev, want)
     assert not np.allclose(s_dev, s_cpu)
+
+
+@pytest.mark.parametrize("layout,batch,seq,text", [("nk", 2, 40, 8), ("nk", 1, 17, 5),
+                                                   ("kn", 2, 24, 6)])
+def test_lm_forward_against_reference(reference, oracle, tmp_path, layout, batch, seq, text):
+    """The oracle's forward (composition of the restated pieces) is bit-identical to
+    the reference's LM::forward (lm.cpp, compiled from source) on an OVW1 file
+    written by ovnative_amd/ovw1.py.  For kn checkpoints the reference CPU takes
+    its non-VNNI fp32-activation kernel (mat.cpp:82-90, no activation
+    quantisation), a different arithmetic; the HIP path computes int8-nk numerics
+    for both layouts, so kn is only checked to stay close (cosine >= 0.9999)."""
+    from lm_fixture import SMALL, make_inputs, make_lm
+    from ovnative_amd import ovw1
+    if not reference.vnni_available():
+        pytest.skip("the reference's int8-nk VNNI path is not available on this host")
+    ts, table = make_lm(5, SMALL, layout=layout)
+    path = str(tmp_path / "lm.ovw")
+    ovw1.write(path, ts)
+    ids, am, attn, pos = make_inputs(6, SMALL, batch, seq, text)
+    h = reference.lm_open(path, SMALL)
+    try:
+        ref = reference.lm_forward(h, SMALL, ids, am, attn, pos)
+    finally:
+        reference.lm_close(h)
+    segs = [(attn[b], seq, b * seq) for b in range(batch)]
+    got = oracle.lm_forward(SMALL, table, ids, am, segs, pos.reshape(-1))
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    ref_flat = ref.transpose(0, 2, 1, 3).reshape(batch * seq, Cb * V)
+    if layout == "nk":
+        assert np.array_equal(bits(got), bits(ref_flat))
+    else:
+        cos = (got.astype(np.float64) * ref_flat).sum() / (
+            np.linalg.norm(got.astype(np.float64)) * np.linalg.norm(ref_flat.astype(np.float64)))
+        assert cos >= 0.9999
