@@ -49,8 +49,15 @@ __global__ __launch_bounds__(256) void quantize_kernel(int64_t M, int64_t K, int
 // computes it (4 rounded squares added in order when >= 4 remain, the rest
 // fused).  Each chain is a sequential dependence of cols/8 fmas; one wavefront
 // per row stages the row in LDS and lanes 0..7 run the chains.
-constexpr int kRmsRowsPerBlock = 4;
+// One wavefront per row; rows_per_block wavefronts share a workgroup.  At the
+// LM's M (hundreds of rows) one row per workgroup spreads the rows over every
+// CU; the kernel is latency-bound (a 1/8-length fma chain per row), so more
+// resident rows is what speeds it up.  Each lane owns the k = 256p + 4*lane..+3
+// elements of quantisation pass p, exactly the elements it loads, so its norm
+// weights for up to kRmsPre passes are prefetched with the row.
+constexpr int kRmsPre = 4;  // cols <= 1024: all weights in registers
 
+template <bool PRE>
 __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int64_t cols,
                                                                int64_t Kb,
                                                                const float* __restrict__ x,
@@ -61,13 +68,33 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
                                                                bool vec4) {
   extern __shared__ float smem[];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * kRmsRowsPerBlock + wave;
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
   const bool active = r < rows;  // every wave still reaches the barriers
   float* xs = smem + (int64_t)wave * (cols + 8);
   float* part = xs + cols;  // 8 partial sums
   const float* row = x + (active ? r : 0) * cols;
+  f32x4 wv[kRmsPre];
+  if (PRE) {
+#pragma unroll
+    for (int p = 0; p < kRmsPre; ++p) {
+      const int64_t k = 256 * p + 4 * lane;
+      wv[p] = k < cols ? *reinterpret_cast<const f32x4*>(w + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
   if (active) {
-    if (vec4) {
+    if (PRE) {  // cols <= 1024: every load in flight before the first LDS store
+      f32x4 xv[kRmsPre];
+#pragma unroll
+      for (int p = 0; p < kRmsPre; ++p) {
+        const int64_t i = 256 * p + 4 * lane;
+        xv[p] = i < cols ? *reinterpret_cast<const f32x4*>(row + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int p = 0; p < kRmsPre; ++p) {
+        const int64_t i = 256 * p + 4 * lane;
+        if (i < cols) *reinterpret_cast<f32x4*>(xs + i) = xv[p];
+      }
+    } else if (vec4) {
       for (int64_t i = lane * 4; i < cols; i += 256) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(row + i);
         xs[i] = v[0]; xs[i + 1] = v[1]; xs[i + 2] = v[2]; xs[i + 3] = v[3];
@@ -80,7 +107,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
   const int64_t nfull = (cols / 8) * 8;
   if (active && lane < 8) {
     float acc = 0.f;
-#pragma unroll 8
+#pragma unroll 16
     for (int64_t i = lane; i < nfull; i += 8) acc = fmaf(xs[i], xs[i], acc);
     part[lane] = acc;
   }
@@ -101,15 +128,25 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
   // across the wavefront so the 8-lane butterflies always see their partners.
   const int grp = lane >> 3, sub = lane & 7;
   int8_t* qrow = aq + r * Kb * 32;
-  for (int64_t b0 = 0; b0 < Kb; b0 += 8) {
+  for (int64_t b0 = 0, p = 0; b0 < Kb; b0 += 8, ++p) {
     const int64_t b = b0 + grp;
     const int64_t k0 = b * 32 + sub * 4;
     const int64_t rem = b < Kb ? cols - k0 : 0;
     const int nvalid = rem >= 4 ? 4 : (rem > 0 ? (int)rem : 0);
     float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (PRE) {
+      f32x4 wp = wv[0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i < nvalid) v[i] = __fmul_rn(__fmul_rn(xs[k0 + i], scale), w[k0 + i]);
+      for (int q = 1; q < kRmsPre; ++q)
+        if (p == q) wp = wv[q];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < nvalid) v[i] = __fmul_rn(__fmul_rn(xs[k0 + i], scale), wp[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < nvalid) v[i] = __fmul_rn(__fmul_rn(xs[k0 + i], scale), w[k0 + i]);
+    }
     uint32_t codes;
     const float s = quant_block_lane(v, nvalid, &codes);
     if (b < Kb) {
@@ -208,19 +245,25 @@ hipError_t launch_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, flo
   return hipGetLastError();
 }
 
+static inline int rms_rows_per_block(int64_t rows) { return rows <= 8192 ? 1 : 4; }
+
 size_t rmsnorm_quantize_smem(int64_t cols) {
-  return sizeof(float) * (size_t)kRmsRowsPerBlock * (size_t)(cols + 8);
+  return sizeof(float) * 4 * (size_t)(cols + 8);  // the largest rows-per-block
 }
 
 hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
                                    float eps, int8_t* aq, float* asc, hipStream_t st) {
   const int64_t Kb = kb_of(cols);
-  const size_t smem = rmsnorm_quantize_smem(cols);
-  const dim3 grid((unsigned)((rows + kRmsRowsPerBlock - 1) / kRmsRowsPerBlock)),
-      block(64 * kRmsRowsPerBlock);
+  const int rpb = rms_rows_per_block(rows);
+  const size_t smem = sizeof(float) * (size_t)rpb * (size_t)(cols + 8);
+  const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(64 * rpb);
   const bool vec4 = cols % 4 == 0 && aligned16(x);
-  hipLaunchKernelGGL(rmsnorm_quantize_kernel, grid, block, smem, st, rows, cols, Kb, x, w, eps,
-                     aq, asc, vec4);
+  if (vec4 && aligned16(w) && cols <= 256 * kRmsPre)
+    hipLaunchKernelGGL(rmsnorm_quantize_kernel<true>, grid, block, smem, st, rows, cols, Kb, x, w,
+                       eps, aq, asc, vec4);
+  else
+    hipLaunchKernelGGL(rmsnorm_quantize_kernel<false>, grid, block, smem, st, rows, cols, Kb, x,
+                       w, eps, aq, asc, vec4);
   return hipGetLastError();
 }
 
