@@ -251,6 +251,25 @@ int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond,
                   int target_len, float guidance, float layer_penalty, int32_t* pred,
                   float* scores);
 
+/* ---- the CFG decoding loop ----------------------------------------------- */
+
+/* The sampling fields of TtsOptions (cpp/src/model/tts.h:26-36); the reference's
+ * defaults are 32, 2.0, 0.1, 5.0, 5.0, 1234. */
+typedef struct OvhGenOptions {
+  int32_t num_steps;
+  float guidance_scale, t_shift, layer_penalty, position_temperature;
+  uint32_t seed;
+} OvhGenOptions;
+
+/* Pipeline::run_sampling (cpp/src/model/tts.cpp:165-364) on the accelerator
+ * branch: the B = 2 CFG batch, `num_steps` forwards with device guided
+ * sampling, Gumbel position noise from std::mt19937(seed), top-k unmasking.
+ * prompt_ids [C, seq] and prompt_audio_mask [seq] as Pipeline::build_prompt
+ * makes them (the last target_len positions hold the mask token); tokens out
+ * [C, target_len], host memory.  Uses the runner's stream; synchronous. */
+int ovh_lm_generate(OvhLm* lm, const int64_t* prompt_ids, const uint8_t* prompt_audio_mask,
+                    int seq, int target_len, const OvhGenOptions* opt, int64_t* tokens);
+
 #if defined(__GNUC__) || defined(__clang__)
 #pragma GCC visibility pop
 #endif

@@ -607,3 +607,85 @@ class Reference:
 
 def reference_available() -> bool:
     return os.path.exists(REF_LIB_PATH)
+
+
+# ---------------------------------------------------------------------------
+# The CFG decoding loop's host logic (cpp/src/model/tts.cpp:165-364), for the
+# tests of ovh_lm_generate.  The per-step forward + guided argmax is passed in
+# (the tests pass the device runner's own, so only this logic is compared).
+
+def mt19937_u32(seed: int, n: int) -> np.ndarray:
+    """n raw outputs of std::mt19937(seed) (init_genrand seeding = numpy's legacy
+    integer seeding; pinned by the C++ standard's known answer, [rand.predef])."""
+    bg = np.random.MT19937()
+    bg._legacy_seeding(seed)
+    return bg.random_raw(n).astype(np.uint32)
+
+
+def uniform_float01(x: np.ndarray) -> np.ndarray:
+    """std::uniform_real_distribution<float>(0, 1) on one 32-bit draw each, as
+    libstdc++'s generate_canonical<float, 24> computes it: float(x) / 2^32,
+    values rounding up to 1 replaced by nextafter(1, 0)."""
+    r = np.asarray(x, np.uint32).astype(np.float32) / np.float32(4294967296.0)
+    return np.where(r >= 1, np.nextafter(np.float32(1), np.float32(0)), r).astype(np.float32)
+
+
+def cfg_schedule(num_steps: int, t_shift: float, total: int):
+    """tts.cpp:231-249: shifted time grid in double from the float option, per-step
+    counts (the last takes the rest)."""
+    import math
+    t_shift = float(np.float32(t_shift))  # TtsOptions::t_shift is a float
+    ts = [t_shift * (i / num_steps) / (1.0 + (t_shift - 1.0) * (i / num_steps))
+          for i in range(num_steps + 1)]
+    sched, rem = [], total
+    for s in range(num_steps):
+        num = rem if s == num_steps - 1 else min(math.ceil(total * (ts[s + 1] - ts[s])), rem)
+        sched.append(int(num))
+        rem -= num
+    return sched
+
+
+def run_sampling(step_fn, prompt_ids, audio_mask, target_len, C_, V, num_steps=32,
+                 guidance=2.0, t_shift=0.1, layer_penalty=5.0, position_temperature=5.0,
+                 seed=1234):
+    """tts.cpp:165-364 (accelerator branch).  step_fn(ids, amask, attn, pos) ->
+    (pred [C, T], scores [C, T]) runs the B = 2 forward and the guided argmax."""
+    libm = C.CDLL("libm.so.6")
+    libm.logf.restype = C.c_float
+    libm.logf.argtypes = [C.c_float]
+    S, T = prompt_ids.shape[1], target_len
+    mask_id = V - 1
+    ids = np.full((2, C_, S), mask_id, np.int64)
+    ids[0] = prompt_ids
+    ids[1, :, :T] = prompt_ids[:, S - T:]
+    am = np.zeros((2, S), np.uint8)
+    am[0] = audio_mask
+    am[1, :T] = 1
+    attn = np.zeros((2, S, S), np.uint8)
+    attn[0] = 1
+    attn[1, :T, :T] = 1
+    attn[1, np.arange(T, S), np.arange(T, S)] = 1
+    pos = np.tile(np.arange(S, dtype=np.int64), (2, 1))
+    tokens = np.full(C_ * T, mask_id, np.int64)
+    draws = iter(uniform_float01(mt19937_u32(seed, num_steps * C_ * T + 1)))
+    for k in cfg_schedule(num_steps, t_shift, C_ * T):
+        if k <= 0:
+            continue
+        pred, scores = step_fn(ids, am, attn, pos)
+        pred = pred.reshape(-1)
+        scores = scores.reshape(-1).astype(np.float32).copy()
+        for i in range(scores.size):
+            u = max(float(next(draws)), float(np.float32(1e-10)))
+            inner = np.float32(-np.float32(libm.logf(u))) + np.float32(1e-10)
+            g = -np.float32(libm.logf(float(inner)))
+            scores[i] = np.float32(scores[i] / np.float32(position_temperature)) + g
+        scores[tokens != mask_id] = -np.inf
+        order = np.argsort(-scores, kind="stable")
+        for idx in order[:min(k, scores.size)]:
+            if not np.isfinite(scores[idx]):
+                break
+            tokens[idx] = pred[idx]
+            c, t = divmod(int(idx), T)
+            ids[0, c, S - T + t] = pred[idx]
+            ids[1, c, t] = pred[idx]
+    return tokens.reshape(C_, T)

@@ -66,7 +66,21 @@ SIGNATURES = {
     "ovh_lm_last_logits": (_p, [_p]),
     "ovh_lm_set_device_sampling": (None, [_p, _int]),
     "ovh_lm_sample": (_int, [_p, _p, _int, _p, _int, _int, _f32, _f32, _p, _p]),
+    "ovh_lm_generate": (_int, [_p, _p, _p, _int, _int, _p, _p]),
 }
+
+
+class GenOptions(C.Structure):
+    """OvhGenOptions = the sampling fields of TtsOptions (cpp/src/model/tts.h:26-36)."""
+    _fields_ = [("num_steps", C.c_int32), ("guidance_scale", C.c_float), ("t_shift", C.c_float),
+                ("layer_penalty", C.c_float), ("position_temperature", C.c_float),
+                ("seed", C.c_uint32)]
+
+    def __init__(self, **kw):
+        d = dict(num_steps=32, guidance_scale=2.0, t_shift=0.1, layer_penalty=5.0,
+                 position_temperature=5.0, seed=1234)
+        d.update(kw)
+        super().__init__(**d)
 
 
 class TensorView(C.Structure):
@@ -491,6 +505,19 @@ class LM:
                                     layer_penalty, pred.ctypes.data, scores.ctypes.data))
         return pred.reshape(self.cfg.n_codebooks, target_len), \
             scores.reshape(self.cfg.n_codebooks, target_len)
+
+    def generate(self, prompt_ids, audio_mask, target_len: int, opts=None):
+        """Pipeline::run_sampling on the device: prompt_ids [C, S] int64, audio_mask [S];
+        returns tokens [C, target_len]."""
+        import numpy as np
+        ids = np.ascontiguousarray(prompt_ids, dtype=np.int64)
+        am = np.ascontiguousarray(audio_mask, dtype=np.uint8)
+        Cb, S = ids.shape
+        out = np.empty((Cb, target_len), np.int64)
+        o = opts if opts is not None else GenOptions()
+        _check(load().ovh_lm_generate(self.handle, ids.ctypes.data, am.ctypes.data, S, target_len,
+                                      C.byref(o), out.ctypes.data))
+        return out
 
     def close(self):
         if getattr(self, "handle", None):

@@ -24,6 +24,8 @@
 #include <cstdint>
 #include <cstring>
 #include <new>
+#include <numeric>
+#include <random>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -730,6 +732,108 @@ int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond,
                          lm->st),
           "download scores");
   OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
+  return OV_OK;
+}
+
+
+// The CFG decoding loop of Pipeline::run_sampling (cpp/src/model/tts.cpp:165-364)
+// on the accelerator branch (use_cuda: the B = 2 batch and the device sampler).
+// Batch: row 0 = the full prompt, row 1 = the target slice of the prompt in its
+// first T positions (full attention among them) and mask tokens attending only
+// to themselves after that.  Schedule ts = t_shift*t / (1 + (t_shift-1)*t), per
+// step ceil(total * (ts[s+1] - ts[s])) positions (the last step takes the rest).
+// Each step: forward, guided argmax per (codebook, frame), Gumbel noise from
+// std::mt19937(seed) / uniform_real_distribution<float>(0, 1) in row-major
+// (codebook, frame) order, already-decoded positions at -inf, then the top-k
+// positions take their predicted token in both rows.
+int ovh_lm_generate(OvhLm* lm, const int64_t* prompt_ids, const uint8_t* prompt_audio_mask,
+                    int seq, int target_len, const OvhGenOptions* opt, int64_t* tokens) {
+  if (!lm || !prompt_ids || !prompt_audio_mask || !opt || !tokens)
+    return set_error(OV_ERR_INVALID_ARG, "generate: null argument");
+  if (seq <= 0 || target_len <= 0 || target_len > seq || opt->num_steps <= 0)
+    return set_error(OV_ERR_INVALID_ARG, "generate: need 0 < target_len <= seq and num_steps > 0");
+  const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab, S = seq, T = target_len;
+  const int64_t mask_id = V - 1;  // kMaskId = 1024 for audio_vocab 1025 (tts.cpp:17)
+  const size_t CS = (size_t)C * S;
+  std::vector<int64_t> ids(2 * CS, mask_id);
+  std::vector<uint8_t> amask(2 * (size_t)S, 0);
+  std::vector<uint8_t> attn(2 * (size_t)S * S, 0);
+  std::vector<int64_t> pos(2 * (size_t)S);
+  std::memcpy(ids.data(), prompt_ids, sizeof(int64_t) * CS);
+  std::memcpy(amask.data(), prompt_audio_mask, (size_t)S);
+  std::fill(attn.begin(), attn.begin() + (size_t)S * S, (uint8_t)1);
+  for (int c = 0; c < C; ++c)
+    for (int t = 0; t < T; ++t)
+      ids[CS + (size_t)c * S + t] = prompt_ids[(size_t)c * S + (S - T + t)];
+  for (int t = 0; t < T; ++t) {
+    amask[(size_t)S + t] = 1;
+    for (int j = 0; j < T; ++j) attn[((size_t)S + t) * S + j] = 1;
+  }
+  for (int t = T; t < S; ++t) attn[((size_t)S + t) * S + t] = 1;
+  for (int b = 0; b < 2; ++b)
+    for (int i = 0; i < S; ++i) pos[(size_t)b * S + i] = i;
+
+  const int steps = opt->num_steps;
+  std::vector<double> ts((size_t)steps + 1);
+  for (int i = 0; i <= steps; ++i) {
+    const double t = (double)i / steps;
+    ts[(size_t)i] = opt->t_shift * t / (1.0 + (opt->t_shift - 1.0) * t);
+  }
+  const int64_t total = (int64_t)T * C;
+  std::vector<int> sched((size_t)steps, 0);
+  int64_t rem = total;
+  for (int st = 0; st < steps; ++st) {
+    const int64_t num =
+        st == steps - 1
+            ? rem
+            : std::min<int64_t>((int64_t)std::ceil(total * (ts[(size_t)st + 1] - ts[(size_t)st])), rem);
+    sched[(size_t)st] = (int)num;
+    rem -= num;
+  }
+
+  std::vector<int64_t> tok((size_t)total, mask_id);
+  std::vector<float> scores((size_t)total);
+  std::vector<int32_t> pred((size_t)total);
+  std::vector<size_t> order((size_t)total);
+  std::mt19937 rng(opt->seed);
+  std::uniform_real_distribution<float> uni(0.f, 1.f);
+  const bool prev = lm->device_sampling;
+  lm->device_sampling = true;
+  int rc = OV_OK;
+  const size_t plane = (size_t)S * C * V;
+  for (int st = 0; st < steps && rc == OV_OK; ++st) {
+    const int k = sched[(size_t)st];
+    if (k <= 0) continue;
+    rc = ovh_lm_forward(lm, 2, S, ids.data(), amask.data(), attn.data(), pos.data(), nullptr);
+    if (rc != OV_OK) break;
+    const float* dev = lm->logits;
+    rc = ovh_lm_sample(lm, dev, S, dev + plane, S, T, opt->guidance_scale, opt->layer_penalty,
+                       pred.data(), scores.data());
+    if (rc != OV_OK) break;
+    for (size_t i = 0; i < scores.size(); ++i) {
+      float u = uni(rng);
+      u = std::max(u, 1e-10f);
+      const float g = -std::log(-std::log(u) + 1e-10f);
+      scores[i] = scores[i] / opt->position_temperature + g;
+    }
+    for (size_t i = 0; i < tok.size(); ++i)
+      if (tok[i] != mask_id) scores[i] = -INFINITY;
+    std::iota(order.begin(), order.end(), (size_t)0);
+    const int kk = std::min<int>(k, (int)order.size());
+    std::partial_sort(order.begin(), order.begin() + kk, order.end(),
+                      [&](size_t a, size_t b) { return scores[a] > scores[b]; });
+    for (int i = 0; i < kk; ++i) {
+      const size_t idx = order[(size_t)i];
+      if (!std::isfinite(scores[idx])) break;
+      tok[idx] = pred[idx];
+      const size_t c = idx / (size_t)T, t = idx % (size_t)T;
+      ids[c * S + (S - T + t)] = pred[idx];
+      ids[CS + c * S + t] = pred[idx];
+    }
+  }
+  lm->device_sampling = prev;
+  if (rc != OV_OK) return rc;
+  std::memcpy(tokens, tok.data(), sizeof(int64_t) * tok.size());
   return OV_OK;
 }
 

@@ -196,3 +196,41 @@ def test_runner_errors(small_lm):
         ov.LM.from_tensors(ts, _cfg(dict(SMALL, head_dim=64)))
     with pytest.raises(ov.InvalidArgument):              # a tensor missing
         ov.LM.from_tensors([t for t in ts if t.name != "llm.norm.weight"], _cfg(SMALL))
+
+
+def test_generate_matches_restated_loop(small_lm):
+    """ovh_lm_generate (the CFG loop on the device runner) against the restated
+    host logic of tts.cpp:165-364 driven by the same runner's forward and
+    sampler: identical tokens."""
+    import oracle
+    import ovnative_amd as ov
+    ts, table, lm = small_lm
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    S, T = 40, 14
+    rng = np.random.default_rng(21)
+    prompt = np.full((Cb, S), V - 1, np.int64)
+    prompt[0, :S - T - 6] = rng.integers(0, SMALL["vocab"], S - T - 6)
+    prompt[:, S - T - 6:S - T] = rng.integers(0, V - 1, (Cb, 6))   # reference frames
+    am = np.zeros(S, np.uint8)
+    am[S - T - 6:] = 1
+    opts = dict(num_steps=8, guidance_scale=2.0, t_shift=0.1, layer_penalty=5.0,
+                position_temperature=5.0, seed=77)
+    got = lm.generate(prompt, am, T, ov.GenOptions(**opts))
+
+    plane = S * Cb * V * 4
+
+    def step(ids, amask, attn, pos):
+        lm.set_device_sampling(True)
+        try:
+            lm.forward(ids, amask, attn, pos, host_logits=False)
+            base = lm.last_logits_ptr()
+            return lm.sample(base, S, base + plane, S, T, opts["guidance_scale"],
+                             opts["layer_penalty"])
+        finally:
+            lm.set_device_sampling(False)
+
+    want = oracle.run_sampling(step, prompt, am, T, Cb, V, num_steps=8, guidance=2.0,
+                               t_shift=0.1, layer_penalty=5.0, position_temperature=5.0,
+                               seed=77)
+    assert np.all(got != V - 1)                       # every position decoded
+    assert np.array_equal(got, want)
