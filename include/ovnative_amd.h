@@ -170,6 +170,16 @@ int ovh_qk_norm_rope(float* q, float* k, const float* qw, const float* kw, int64
 int ovh_attention(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_heads,
                   int head_dim, const float* q, int64_t q_stride, const float* k, const float* v,
                   int64_t kv_stride, float scale, float* out, int64_t out_stride, void* stream);
+/* The same attention with the products split into f16 hi/lo parts on the f16
+ * matrix core (hi*hi + hi*lo + lo*hi, ~2^-22 relative; 5x less matrix-core
+ * time than the fp32 form).  No reference counterpart beyond ovh_attention's.
+ * |k| and |v| must stay below 65504 (OV_ERR_INVALID_ARG otherwise); strides a
+ * multiple of 8, kv_off a whole number of rows, at most 32 segments.  Allocates
+ * its split workspace stream-ordered and synchronises the stream. */
+int ovh_attention_split(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_heads,
+                        int head_dim, const float* q, int64_t q_stride, const float* k,
+                        const float* v, int64_t kv_stride, float scale, float* out,
+                        int64_t out_stride, void* stream);
 
 /* ---- weights: OVW1 files -------------------------------------------------- */
 
@@ -245,6 +255,10 @@ int ovh_lm_forward_cfg(OvhLm* lm, int cond_seq, int uncond_seq, const int64_t* i
 const void* ovh_lm_last_logits(const OvhLm* lm);
 /* LmRunnerSetDeviceSampling (cuda_lm.h:46). */
 void ovh_lm_set_device_sampling(OvhLm* lm, int on);
+/* Attention kernel of the runner: 1 = split-f16 products (default), 0 = fp32
+ * products.  No reference counterpart (the CUDA runner picks its attention
+ * kernel from the sequence length and environment variables, cuda_lm.cu:1106-1115). */
+void ovh_lm_set_attention(OvhLm* lm, int split_f16);
 /* LmRunnerSampleThunk (cuda_lm.h:39-41): the per-step guidance + argmax pass
  * (tts.cpp:296-326) on device logit planes; pred/scores host [C, target_len]. */
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

@@ -67,6 +67,9 @@ SIGNATURES = {
     "ovh_lm_set_device_sampling": (None, [_p, _int]),
     "ovh_lm_sample": (_int, [_p, _p, _int, _p, _int, _int, _f32, _f32, _p, _p]),
     "ovh_lm_generate": (_int, [_p, _p, _p, _int, _int, _p, _p]),
+    "ovh_attention_split": (_int, [_p, _int, _int, _int, _int, _p, _i64, _p, _p, _i64, _f32, _p,
+                                   _i64, _p]),
+    "ovh_lm_set_attention": (None, [_p, _int]),
 }
 
 
@@ -341,7 +344,7 @@ def qk_norm_rope(q, k, qw, kw, n_heads: int, n_kv_heads: int, head_dim: int, cos
 
 
 def attention(q, k, v, segs, n_heads: int, n_kv_heads: int, head_dim: int = 128, scale=None,
-              out=None):
+              out=None, split: bool = False):
     """GQA attention over segments (LM::run_layer's loop over attention_head_f32).
 
     segs: list of (bias tensor [rows, rows] or None, rows, q_row0, kv_row0) with row
@@ -355,9 +358,10 @@ def attention(q, k, v, segs, n_heads: int, n_kv_heads: int, head_dim: int = 128,
     for i, (bias, rows, qr, kr) in enumerate(segs):
         arr[i] = AttnSegment(0 if bias is None else _dptr(bias).value, rows,
                              qr * q.stride(0), kr * k.stride(0))
-    _check(load().ovh_attention(C.cast(arr, C.c_void_p), len(segs), n_heads, n_kv_heads,
-                                head_dim, _dptr(q), q.stride(0), _dptr(k), _dptr(v), k.stride(0),
-                                scale, _dptr(out), out.stride(0), _stream()))
+    fn = load().ovh_attention_split if split else load().ovh_attention
+    _check(fn(C.cast(arr, C.c_void_p), len(segs), n_heads, n_kv_heads, head_dim, _dptr(q),
+              q.stride(0), _dptr(k), _dptr(v), k.stride(0), scale, _dptr(out), out.stride(0),
+              _stream()))
     return out
 
 
@@ -493,6 +497,9 @@ class LM:
 
     def set_device_sampling(self, on: bool) -> None:
         load().ovh_lm_set_device_sampling(self.handle, int(bool(on)))
+
+    def set_attention(self, split_f16: bool) -> None:
+        load().ovh_lm_set_attention(self.handle, int(bool(split_f16)))
 
     def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
                target_len: int, guidance: float, layer_penalty: float):

@@ -14,6 +14,10 @@ struct AttnSeg {
   int32_t rows;
   int64_t q_off;      // element offset into q and out
   int64_t kv_off;     // element offset into k and v
+  // Split-f16 kernel, mask form (launch_attention_split_only with mask_bits):
+  // bit t % 32 of word [row * ((rows + 31) / 32) + t / 32] set = key t visible
+  // (bias 0), clear = bias -1e30; nullptr = no mask.
+  const uint32_t* bits;
 };
 
 struct AttnArgs {
@@ -38,5 +42,42 @@ hipError_t launch_qk_norm_rope(float* q, float* k, const float* qw, const float*
                                hipStream_t st);
 // head_dim 128; args.n_segs <= kAttnMaxSegs; max_rows = largest segment.
 hipError_t launch_attention(const AttnArgs& args, int max_rows, hipStream_t st);
+
+// Split-f16 attention (three f16 matrix-core products per fp32 product).
+// K and V are split once per call into f16 hi/lo planes:
+//   kh, kl : [T][kv_stride] row-major, the rows of k (same row indexing);
+//   vh, vl : [kv_heads*128][vt_cols] transposed, each segment's keys starting at
+//            column vt_off[s] (a multiple of 32, rows padded with zeros), keys
+//            permuted inside every 16-key group (bits 2 and 3 of the index
+//            swapped) and head-dim rows permuted (row 32j + r holds d = 4r + j)
+//            into the order the P.V matrix-core operands read them.
+// vt_off[s] = sum over earlier segments of round_up(rows, 32).
+struct AttnSplit {
+  _Float16* kh;
+  _Float16* kl;
+  _Float16* vh;
+  _Float16* vl;
+  int64_t vt_cols;
+  int64_t vt_off[kAttnMaxSegs];
+  int32_t n_kv_heads;
+  uint32_t* overflow;  // set non-zero when a |k| or |v| is beyond the f16 range
+};
+// Splits K (the rows the segments cover) and V into the planes, then attends.
+hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                  hipStream_t st);
+// Attention alone, over planes already written (launch_qk_norm_rope_split); the
+// segments' masks from AttnSeg::bits when mask_bits, else from AttnSeg::bias.
+hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                       bool mask_bits, hipStream_t st);
+// uint8 mask [rows, rows] (non-zero = visible) -> AttnSeg::bits words.
+hipError_t launch_mask_bits(const uint8_t* mask, int rows, uint32_t* bits, hipStream_t st);
+// launch_qk_norm_rope (D = 128) that also writes the planes of the roped k rows
+// (sp.kh/kl at k's indexing, args.kv_stride = n_kv_heads * 128) and of the V
+// tiles of args' segments, in one launch.
+hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const float* kw,
+                                     int64_t rows, int n_heads, int n_kv_heads,
+                                     const float* cos_tab, const float* sin_tab, float eps,
+                                     const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                     hipStream_t st);
 
 }  // namespace ovh

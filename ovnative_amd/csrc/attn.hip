@@ -1,5 +1,7 @@
 // Attention side of one decoder layer for gfx950: RoPE tables, fused per-head
 // RMSNorm + RoPE, and bidirectional GQA attention with an additive bias.
+#include <cstdint>
+
 #include "attn.h"
 #include "ovh_common.h"
 
@@ -40,6 +42,41 @@ hipError_t launch_rope_tables(int64_t rows, const int64_t* pos, int D, float the
 // rotation pair (t, t + D/2).  The sum of squares reproduces the reference's
 // 8-lane fma accumulator: chain j takes elements j, j+8, ... in order, and the
 // 8 chains are added left to right, so the norm scale is the reference's bits.
+// Lane t < D/2 of the wavefront returns the normalised, rotated pair (t, t + D/2)
+// of the head vector v in (oa, ob); the other lanes return false.
+template <int D>
+__device__ __forceinline__ bool norm_rope_pair(const float* __restrict__ v,
+                                               const float* __restrict__ w,
+                                               const float* __restrict__ cos_row,
+                                               const float* __restrict__ sin_row, float eps,
+                                               int lane, float& oa, float& ob) {
+  constexpr int half = D / 2;
+  const bool own = lane < half;
+  const float a = own ? v[lane] : 0.f;
+  const float b = own ? v[lane + half] : 0.f;
+
+  // Chain j = lane % 8 (lanes 8.. compute copies that are not used).
+  const int j = lane & 7;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    const int d = j + 8 * i;
+    const float x = (8 * i < half) ? __shfl(a, d) : __shfl(b, d - half);
+    s = fmaf(x, x, s);
+  }
+  float sum = __shfl(s, 0);
+#pragma unroll
+  for (int c = 1; c < 8; ++c) sum = __fadd_rn(sum, __shfl(s, c));
+  const float scale = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)D), eps)));
+  if (!own) return false;
+  const float c = cos_row[lane], sn = sin_row[lane];
+  const float na = __fmul_rn(__fmul_rn(a, scale), w[lane]);
+  const float nb = __fmul_rn(__fmul_rn(b, scale), w[lane + half]);
+  oa = fmaf(na, c, -__fmul_rn(nb, sn));
+  ob = fmaf(na, sn, __fmul_rn(nb, c));
+  return true;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(float* __restrict__ q,
                                                            float* __restrict__ k,
@@ -58,30 +95,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(float* __restrict__ q
   const int64_t r = task / heads;
   const int h = (int)(task - r * heads);
   float* v = h < n_heads ? q + (r * n_heads + h) * D : k + (r * n_kv_heads + (h - n_heads)) * D;
-  const float* w = h < n_heads ? qw : kw;
-  const bool own = lane < half;
-  const float a = own ? v[lane] : 0.f;
-  const float b = own ? v[lane + half] : 0.f;
-
-  // Chain j = lane % 8 (lanes 8.. compute copies that are not used).
-  const int j = lane & 7;
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < D / 8; ++i) {
-    const int d = j + 8 * i;
-    const float x = (8 * i < half) ? __shfl(a, d) : __shfl(b, d - half);
-    s = fmaf(x, x, s);
-  }
-  float sum = __shfl(s, 0);
-#pragma unroll
-  for (int c = 1; c < 8; ++c) sum = __fadd_rn(sum, __shfl(s, c));
-  const float scale = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)D), eps)));
-  if (!own) return;
-  const float c = cos_tab[r * half + lane], sn = sin_tab[r * half + lane];
-  const float na = __fmul_rn(__fmul_rn(a, scale), w[lane]);
-  const float nb = __fmul_rn(__fmul_rn(b, scale), w[lane + half]);
-  v[lane] = fmaf(na, c, -__fmul_rn(nb, sn));
-  v[lane + half] = fmaf(na, sn, __fmul_rn(nb, c));
+  float oa, ob;
+  if (!norm_rope_pair<D>(v, h < n_heads ? qw : kw, cos_tab + r * half, sin_tab + r * half, eps,
+                         lane, oa, ob))
+    return;
+  v[lane] = oa;
+  v[lane + half] = ob;
 }
 
 hipError_t launch_qk_norm_rope(float* q, float* k, const float* qw, const float* kw,
@@ -285,6 +304,512 @@ hipError_t launch_attention(const AttnArgs& args, int max_rows, hipStream_t st) 
   const dim3 grid((unsigned)((max_rows + kAttnQ - 1) / kAttnQ), (unsigned)args.n_heads,
                   (unsigned)args.n_segs);
   hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, st, args);
+  return hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------
+// Split-f16 attention.  fp32 x = hi + lo with hi = f16(x) and lo = f16(x - hi):
+// hi*hi + hi*lo + lo*hi carries the product to ~2^-22 relative (lo*lo is
+// dropped), and each term is exact in the fp32 accumulator, so three
+// V_MFMA_F32_32X32X16_F16 replace eight V_MFMA_F32_32X32X2_F32 per 32x32x16
+// product: 5.3x less matrix-core time than the fp32 kernel above, same
+// structure otherwise.  Values beyond the f16 range would become inf: the split
+// pass reports them through `overflow` (the reference's own GPU path runs its
+// activations in fp16 too, cuda_lm.cu:1086-1160).
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split16(float x, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+
+__device__ __forceinline__ f32x16 mfma_h(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// ---- f16 hi/lo planes of K and V --------------------------------------------
+// K: element i of the k rows -> kh[i], kl[i] (same row indexing and stride).
+__device__ __forceinline__ bool split_k8(const float* __restrict__ src, _Float16* __restrict__ dh,
+                                         _Float16* __restrict__ dl) {
+  const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
+  const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
+  h8 h, l;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float x = j < 4 ? x0[j] : x1[j - 4];
+    bad |= !(fabsf(x) < 65504.f);
+    _Float16 a, b;
+    split16(x, a, b);
+    h[j] = a;
+    l[j] = b;
+  }
+  *reinterpret_cast<h8*>(dh) = h;
+  *reinterpret_cast<h8*>(dl) = l;
+  return bad;
+}
+
+// V: one 32-key x 32-dim tile (key tile `kt` of segment `s`, dims 32*dq..+31 of
+// KV head `kvh`) through LDS.  Output row 32j + r of a head holds d = 4r + j;
+// column vt_off[s] + key with bits 2 and 3 swapped; keys past the segment are 0.
+// `tile` is 32 x 33 floats of LDS.  Returns true when a value is beyond f16.
+__device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit& sp, int s, int kt,
+                                             int kvh, int dq, float (*tile)[33]) {
+  const AttnSeg seg = a.segs[s];
+  const int t0 = kt * 32;
+  {
+    const int key = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t0 + key < seg.rows)
+      x = *reinterpret_cast<const f32x4*>(a.v + seg.kv_off + (int64_t)(t0 + key) * a.kv_stride +
+                                          kvh * kAttnD + dq * 32 + c4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[key][c4 + j] = x[j];
+  }
+  __syncthreads();
+  bool bad = false;
+  if (threadIdx.x < 128) {
+    const int dl = threadIdx.x >> 2, kg = threadIdx.x & 3;
+    const int d = dq * 32 + dl;
+    h8 h, l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = 8 * kg + i;                                        // stored position
+      const int key = (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);     // swap bits 2 and 3
+      const float x = tile[key][dl];
+      bad |= !(fabsf(x) < 65504.f);
+      _Float16 hi, lo;
+      split16(x, hi, lo);
+      h[i] = hi;
+      l[i] = lo;
+    }
+    const int64_t orow = (int64_t)kvh * kAttnD + 32 * (d & 3) + (d >> 2);
+    const int64_t col = sp.vt_off[s] + t0 + 8 * kg;
+    *reinterpret_cast<h8*>(sp.vh + orow * sp.vt_cols + col) = h;
+    *reinterpret_cast<h8*>(sp.vl + orow * sp.vt_cols + col) = l;
+  }
+  return bad;
+}
+
+// V tiles of one launch: blockIdx -> (segment, key tile, kv head, dim quarter).
+__device__ __forceinline__ bool split_v_job(const AttnArgs& a, const AttnSplit& sp, int64_t job,
+                                            int ktiles, float (*tile)[33]) {
+  const int per_seg = ktiles * sp.n_kv_heads * 4;
+  const int s = (int)(job / per_seg);
+  int r = (int)(job - (int64_t)s * per_seg);
+  const int kt = r / (sp.n_kv_heads * 4);
+  r -= kt * sp.n_kv_heads * 4;
+  if (kt * 32 >= a.segs[s].rows) return false;  // uniform for the workgroup
+  return split_v_tile(a, sp, s, kt, r >> 2, r & 3, tile);
+}
+
+// Standalone split of K (rows [r_lo, r_lo + k_rows)) and V for one attention call:
+// the first k_blocks workgroups take 2048 K elements each, the rest one V tile.
+__global__ __launch_bounds__(256) void split_kv_kernel(AttnArgs a, AttnSplit sp, int64_t r_lo,
+                                                       int64_t k_rows, int64_t k_blocks,
+                                                       int ktiles) {
+  __shared__ float tile[32][33];
+  bool bad = false;
+  if ((int64_t)blockIdx.x < k_blocks) {
+    const int64_t width = (int64_t)sp.n_kv_heads * kAttnD;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    const int64_t r = i / width, c = i - r * width;
+    if (r < k_rows) {
+      const int64_t off = (r_lo + r) * a.kv_stride + c;
+      bad = split_k8(a.k + off, sp.kh + off, sp.kl + off);
+    }
+  } else {
+    bad = split_v_job(a, sp, (int64_t)blockIdx.x - k_blocks, ktiles, tile);
+  }
+  if (bad) atomicOr(sp.overflow, 1u);
+}
+
+// The runner's form: per-head RMSNorm + RoPE of q and k (as qk_norm_rope_kernel,
+// one wavefront per (row, head)) that also writes the f16 planes of the roped k,
+// and, in the workgroups past the q/k ones, the V tiles.
+__global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
+    float* __restrict__ q, float* __restrict__ k, const float* __restrict__ qw,
+    const float* __restrict__ kw, int64_t rows, int n_heads, int n_kv_heads,
+    const float* __restrict__ cos_tab, const float* __restrict__ sin_tab, float eps,
+    int64_t qk_blocks, int ktiles, AttnArgs a, AttnSplit sp) {
+  __shared__ float tile[32][33];
+  if ((int64_t)blockIdx.x >= qk_blocks) {
+    if (split_v_job(a, sp, (int64_t)blockIdx.x - qk_blocks, ktiles, tile))
+      atomicOr(sp.overflow, 1u);
+    return;
+  }
+  constexpr int D = kAttnD, half = D / 2;
+  const int lane = threadIdx.x & 63;
+  const int heads = n_heads + n_kv_heads;
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= rows * heads) return;
+  const int64_t r = task / heads;
+  const int h = (int)(task - r * heads);
+  const bool is_k = h >= n_heads;
+  const int64_t off = is_k ? (r * n_kv_heads + (h - n_heads)) * D : (r * n_heads + h) * D;
+  float* v = (is_k ? k : q) + off;
+  float oa, ob;
+  if (!norm_rope_pair<D>(v, is_k ? kw : qw, cos_tab + r * half, sin_tab + r * half, eps, lane, oa, ob))
+    return;
+  v[lane] = oa;
+  v[lane + half] = ob;
+  if (is_k) {
+    _Float16 h0, l0, h1, l1;
+    split16(oa, h0, l0);
+    split16(ob, h1, l1);
+    sp.kh[off + lane] = h0;
+    sp.kl[off + lane] = l0;
+    sp.kh[off + lane + half] = h1;
+    sp.kl[off + lane + half] = l1;
+    if (!(fabsf(oa) < 65504.f) || !(fabsf(ob) < 65504.f)) atomicOr(sp.overflow, 1u);
+  }
+}
+
+// Attention over the planes.  Same work split as attention_kernel (one
+// workgroup per (segment, head, 32 queries), 4 wavefronts over 32-key blocks,
+// merged through LDS); the Q planes of the workgroup sit in LDS, the softmax
+// runs in base 2 (scores scaled by log2(e), V_EXP_F32), and each wavefront loads
+// the K and V fragments of its next block while it computes the current one.
+constexpr int kQPad = kAttnD + 8;  // LDS row of a Q plane, in halves
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kMaskedLog2 = -1e29f * kLog2e;
+
+template <bool kBits>
+__global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, AttnSplit sp) {
+  // The Q planes (2 x 32 x kQPad halves) alias the start of `part`, which is
+  // written only after every wavefront has left the key loop.
+  __shared__ __attribute__((aligned(16))) float part[kAttnWaves][kAttnQ][kAttnD];
+  __shared__ float mstat[kAttnWaves][kAttnQ], lstat[kAttnWaves][kAttnQ];
+  __shared__ float alpha_s[kAttnWaves][kAttnQ];
+  _Float16* qs_h = reinterpret_cast<_Float16*>(&part[0][0][0]);
+  _Float16* qs_l = qs_h + kAttnQ * kQPad;
+
+  const AttnSeg seg = args.segs[blockIdx.z];
+  const int S = seg.rows;
+  const int q0 = blockIdx.x * kAttnQ;
+  if (q0 >= S) return;
+  const int h = blockIdx.y, kvh = h / args.group;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+
+  // ---- Q rows q0..q0+31 of head h -> hi/lo planes in LDS (16 values per thread)
+  {
+    const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 16;
+    const int qr = min(q0 + row, S - 1);
+    const float* src = args.q + seg.q_off + (int64_t)qr * args.q_stride + (int64_t)h * kAttnD + c0;
+    h8 hh[2], ll[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(src + 4 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        _Float16 a, b;
+        split16(x[e], a, b);
+        hh[j >> 1][4 * (j & 1) + e] = a;
+        ll[j >> 1][4 * (j & 1) + e] = b;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      *reinterpret_cast<h8*>(qs_h + row * kQPad + c0 + 8 * j) = hh[j];
+      *reinterpret_cast<h8*>(qs_l + row * kQPad + c0 + 8 * j) = ll[j];
+    }
+  }
+
+  // Wave-uniform plane bases and 32-bit per-lane element offsets (the launcher
+  // checks that every offset fits).
+  const int64_t krow0 = seg.kv_off / args.kv_stride;  // segment's first k row
+  const _Float16* __restrict__ khb = sp.kh + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
+  const _Float16* __restrict__ klb = sp.kl + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
+  const int64_t vbase = (int64_t)kvh * kAttnD * sp.vt_cols + sp.vt_off[blockIdx.z];
+  const _Float16* __restrict__ vhb = sp.vh + vbase;
+  const _Float16* __restrict__ vlb = sp.vl + vbase;
+  const uint32_t vlane = (uint32_t)(r32 * sp.vt_cols + 8 * hf);
+  const uint32_t vstep = 32u * (uint32_t)sp.vt_cols;  // 32 head-dim rows of the V planes
+  const uint32_t kstride = (uint32_t)args.kv_stride;
+
+  // Mask of this lane's query row: bit words (kBits) or the additive bias row.
+  const int qrow = min(q0 + r32, S - 1);
+  const uint32_t* mrow =
+      kBits && seg.bits ? seg.bits + (int64_t)qrow * ((S + 31) >> 5) : nullptr;
+  const float* brow = !kBits && seg.bias ? seg.bias + (int64_t)qrow * S : nullptr;
+  const bool bias_vec = brow && (S & 3) == 0 && (reinterpret_cast<uintptr_t>(seg.bias) & 15) == 0;
+  const float sl2 = args.scale * kLog2e;
+  constexpr float kMaskedBias = -1e30f * kLog2e;  // the mask's bias, in base-2 units
+
+  h8 kh[8], kl[8], vh[8], vl[8];  // K: chunk c; V: 8 * (16-key chunk) + ... index 4c + db
+  auto load_k = [&](int t0) {
+    const uint32_t off = (uint32_t)min(t0 + r32, S - 1) * kstride + 8 * hf;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      kh[c] = *reinterpret_cast<const h8*>(khb + (off + 16 * c));
+      kl[c] = *reinterpret_cast<const h8*>(klb + (off + 16 * c));
+    }
+  };
+  auto load_v = [&](int t0) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint32_t off = vlane + db * vstep + (uint32_t)(t0 + 16 * c);
+        vh[4 * c + db] = *reinterpret_cast<const h8*>(vhb + off);
+        vl[4 * c + db] = *reinterpret_cast<const h8*>(vlb + off);
+      }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[c][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // The mask form prefetches the next block's K and V; the float-bias form has
+  // 16 more live values per lane and loads K and V at the start of each block.
+  constexpr bool kPrefetch = kBits;
+  const int nblk = (S + kAttnK - 1) / kAttnK;
+  if (kPrefetch && wave < nblk) {
+    load_k(wave * kAttnK);
+    load_v(wave * kAttnK);
+  }
+  __syncthreads();  // Q planes written
+
+  for (int blk = wave; blk < nblk; blk += kAttnWaves) {
+    const int t0 = blk * kAttnK;
+    const bool more = kPrefetch && blk + kAttnWaves < nblk;  // uniform for the wavefront
+    if (!kPrefetch) {
+      load_k(t0);
+      load_v(t0);
+    }
+    // this lane's 16 mask bits: bit 8g + i = key t0 + 8g + 4hf + i
+    const uint32_t mword = (mrow ? mrow[blk] : 0xffffffffu) >> (4 * hf);
+    // ---- S^T = K Q^T (32 keys x 32 queries), three f16 products per chunk
+    f32x16 st;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st[e] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const h8 qh = *reinterpret_cast<const h8*>(qs_h + r32 * kQPad + 16 * c + 8 * hf);
+      const h8 ql = *reinterpret_cast<const h8*>(qs_l + r32 * kQPad + 16 * c + 8 * hf);
+      st = mfma_h(kl[c], qh, st);
+      st = mfma_h(kh[c], ql, st);
+      st = mfma_h(kh[c], qh, st);
+    }
+    // the next block's fragments reuse these registers: keep the loads after
+    // the products that read them
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) load_k(t0 + kAttnWaves * kAttnK);
+
+    // bias of this lane's 16 keys (key of element e: t0 + 8(e/4) + 4hf + e%4),
+    // base-2 units
+    float bv[16];
+    if (kBits) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+    } else if (brow) {
+      if (bias_vec) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int tg = t0 + 8 * g + 4 * hf;
+          f32x4 b4 = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (tg < S) b4 = *reinterpret_cast<const f32x4*>(brow + tg);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[4 * g + e] = b4[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bv[e] = brow[min(t0 + 8 * (e >> 2) + 4 * hf + (e & 3), S - 1)];
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bv[e] = __fmul_rn(bv[e], kLog2e);
+    }
+
+    // ---- base-2 softmax statistics
+    float p[16];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int t = t0 + 8 * (e >> 2) + 4 * hf + (e & 3);
+      float y = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
+      y = t < S ? y : -INFINITY;
+      p[e] = y;
+      bmax = fmaxf(bmax, y);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float m_new = fmaxf(m_run, bmax);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // all keys so far at -inf
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = __builtin_amdgcn_exp2f(p[e] - m_ref);
+      psum = __fadd_rn(psum, p[e]);
+    }
+    psum = __fadd_rn(psum, __shfl_xor(psum, 32));
+    l_run = fmaf(l_run, alpha, psum);
+    m_run = m_new;
+
+    if (hf == 0) alpha_s[wave][r32] = alpha;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&alpha_s[wave][8 * g + 4 * hf]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- O += P V: 16-key chunk c takes this lane's p[8c .. 8c+7]
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      h8 ph, pl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 a, b;
+        split16(p[8 * c + j], a, b);
+        ph[j] = a;
+        pl[j] = b;
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        o[db] = mfma_h(pl, vh[4 * c + db], o[db]);
+        o[db] = mfma_h(ph, vl[4 * c + db], o[db]);
+        o[db] = mfma_h(ph, vh[4 * c + db], o[db]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) load_v(t0 + kAttnWaves * kAttnK);
+  }
+
+  __syncthreads();  // every wavefront is done with the Q planes
+  // merge the 4 key splits (output column of block db, lane r32: d = 4*r32 + db)
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const int i = 8 * (e >> 2) + 4 * hf + (e & 3);
+    f32x4 w4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w4[c] = o[c][e];
+    *reinterpret_cast<f32x4*>(&part[wave][i][4 * r32]) = w4;
+  }
+  if (hf == 0) {
+    mstat[wave][r32] = m_run;
+    lstat[wave][r32] = l_run;
+  }
+  __syncthreads();
+  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
+  if (q0 + qi >= S) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mstat[w][qi]);
+  float* dst = args.out + seg.q_off + (int64_t)(q0 + qi) * args.out_stride + (int64_t)h * kAttnD + d0;
+  if (M < kMaskedLog2) {  // fully masked row (largest biased score below -1e29)
+#pragma unroll
+    for (int j = 0; j < 16; j += 4) *reinterpret_cast<f32x4*>(dst + j) = f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  float f[kAttnWaves], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) {
+    f[w] = mstat[w][qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mstat[w][qi] - M);
+    L = fmaf(lstat[w][qi], f[w], L);
+  }
+  const float inv = __fdiv_rn(1.f, L);
+#pragma unroll
+  for (int j = 0; j < 16; j += 4) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&part[w][qi][d0 + j]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = fmaf(x[c], f[w], acc[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = __fmul_rn(acc[c], inv);
+    *reinterpret_cast<f32x4*>(dst + j) = acc;
+  }
+}
+
+hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                  hipStream_t st) {
+  if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
+  // K: the rows the segments cover, as one range [first row, last row]
+  int64_t r_lo = INT64_MAX, r_hi = 0;
+  for (int i = 0; i < args.n_segs; ++i) {
+    if (args.segs[i].rows <= 0) continue;
+    const int64_t r0 = args.segs[i].kv_off / args.kv_stride;
+    r_lo = r0 < r_lo ? r0 : r_lo;
+    r_hi = r0 + args.segs[i].rows > r_hi ? r0 + args.segs[i].rows : r_hi;
+  }
+  if (r_hi <= r_lo) return hipSuccess;
+  const int64_t width = (int64_t)sp.n_kv_heads * kAttnD;
+  const int64_t k_blocks = ((r_hi - r_lo) * width / 8 + 255) / 256;
+  const int ktiles = (max_rows + 31) / 32;
+  const int64_t v_jobs = (int64_t)args.n_segs * ktiles * sp.n_kv_heads * 4;
+  hipLaunchKernelGGL(split_kv_kernel, dim3((unsigned)(k_blocks + v_jobs)), dim3(256), 0, st, args,
+                     sp, r_lo, r_hi - r_lo, k_blocks, ktiles);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_attention_split_only(args, sp, max_rows, false, st);
+}
+
+hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                       bool mask_bits, hipStream_t st) {
+  if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
+  // per-lane plane offsets are 32-bit
+  if ((uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
+      (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((max_rows + kAttnQ - 1) / kAttnQ), (unsigned)args.n_heads,
+                  (unsigned)args.n_segs);
+  if (mask_bits)
+    hipLaunchKernelGGL(attention_split_kernel<true>, grid, dim3(256), 0, st, args, sp);
+  else
+    hipLaunchKernelGGL(attention_split_kernel<false>, grid, dim3(256), 0, st, args, sp);
+  return hipGetLastError();
+}
+
+// One thread per 32-key word of a mask row.
+__global__ __launch_bounds__(256) void mask_bits_kernel(const uint8_t* __restrict__ mask, int rows,
+                                                        uint32_t* __restrict__ bits) {
+  const int words = (rows + 31) >> 5;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)rows * words) return;
+  const int64_t r = i / words;
+  const int w = (int)(i - r * words);
+  const uint8_t* src = mask + r * rows + 32 * w;
+  const int n = min(32, rows - 32 * w);
+  uint32_t b = 0;
+  for (int j = 0; j < n; ++j) b |= (src[j] != 0 ? 1u : 0u) << j;
+  bits[i] = b;
+}
+
+hipError_t launch_mask_bits(const uint8_t* mask, int rows, uint32_t* bits, hipStream_t st) {
+  const int64_t n = (int64_t)rows * ((rows + 31) / 32);
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(mask_bits_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, mask,
+                     rows, bits);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const float* kw,
+                                     int64_t rows, int n_heads, int n_kv_heads,
+                                     const float* cos_tab, const float* sin_tab, float eps,
+                                     const AttnArgs& args, const AttnSplit& sp, int max_rows,
+                                     hipStream_t st) {
+  const int64_t tasks = rows * (n_heads + n_kv_heads);
+  if (tasks <= 0) return hipSuccess;
+  const int64_t qk_blocks = (tasks + 3) / 4;
+  const int ktiles = (max_rows + 31) / 32;
+  const int64_t v_jobs = args.n_segs > 0 ? (int64_t)args.n_segs * ktiles * sp.n_kv_heads * 4 : 0;
+  hipLaunchKernelGGL(qk_norm_rope_split_kernel, dim3((unsigned)(qk_blocks + v_jobs)), dim3(256), 0,
+                     st, q, k, qw, kw, rows, n_heads, n_kv_heads, cos_tab, sin_tab, eps, qk_blocks,
+                     ktiles, args, sp);
   return hipGetLastError();
 }
 

@@ -397,11 +397,74 @@ int ovh_attention(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_
     int max_rows = 0;
     for (int i = 0; i < a.n_segs; ++i) {
       const OvhAttnSegment& g = segs[s0 + i];
-      a.segs[i] = ovh::AttnSeg{g.bias, g.rows, g.q_off, g.kv_off};
+      a.segs[i] = ovh::AttnSeg{g.bias, g.rows, g.q_off, g.kv_off, nullptr};
       max_rows = g.rows > max_rows ? g.rows : max_rows;
     }
     OVH_HIP(ovh::launch_attention(a, max_rows, as_stream(stream)), "attention launch");
   }
+  return OV_OK;
+}
+
+int ovh_attention_split(const OvhAttnSegment* segs, int n_segs, int n_heads, int n_kv_heads,
+                        int head_dim, const float* q, int64_t q_stride, const float* k,
+                        const float* v, int64_t kv_stride, float scale, float* out,
+                        int64_t out_stride, void* stream) {
+  if (n_segs <= 0) return OV_OK;
+  if (n_segs > ovh::kAttnMaxSegs)
+    return fail(OV_ERR_INVALID_ARG, "attention_split: at most 32 segments per call");
+  if (!segs) return fail(OV_ERR_INVALID_ARG, "segs is null");
+  if (head_dim != 128) return fail(OV_ERR_NOT_IMPLEMENTED, "attention: head_dim must be 128");
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 65535)
+    return fail(OV_ERR_INVALID_ARG, "attention: n_heads must be a positive multiple of n_kv_heads");
+  if (!q || !k || !v || !out) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (q_stride < (int64_t)n_heads * head_dim || out_stride < (int64_t)n_heads * head_dim ||
+      kv_stride < (int64_t)n_kv_heads * head_dim)
+    return fail(OV_ERR_INVALID_ARG, "attention: row strides smaller than the head span");
+  if ((q_stride | kv_stride | out_stride) & 7)
+    return fail(OV_ERR_INVALID_ARG, "attention_split: strides must be multiples of 8 elements");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u)
+    return fail(OV_ERR_INVALID_ARG, "attention: q/k/v/out must be 16-byte aligned");
+  ovh::AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.out = out;
+  a.q_stride = q_stride; a.kv_stride = kv_stride; a.out_stride = out_stride;
+  a.n_heads = n_heads; a.group = n_heads / n_kv_heads; a.scale = scale; a.n_segs = n_segs;
+  ovh::AttnSplit sp{};
+  int max_rows = 0;
+  int64_t rows_hi = 0;
+  for (int s = 0; s < n_segs; ++s) {
+    const OvhAttnSegment& g = segs[s];
+    if (g.rows < 0 || g.q_off < 0 || g.kv_off < 0 || (g.q_off & 7) || g.kv_off % kv_stride)
+      return fail(OV_ERR_INVALID_ARG, "attention_split: bad segment (rows/offsets; kv_off must "
+                                      "be a whole number of k rows)");
+    a.segs[s] = ovh::AttnSeg{g.bias, g.rows, g.q_off, g.kv_off, nullptr};
+    sp.vt_off[s] = sp.vt_cols;
+    sp.vt_cols += (g.rows + 31) / 32 * 32;
+    max_rows = g.rows > max_rows ? g.rows : max_rows;
+    const int64_t end = g.kv_off / kv_stride + g.rows;
+    rows_hi = end > rows_hi ? end : rows_hi;
+  }
+  sp.n_kv_heads = n_kv_heads;
+  hipStream_t st = as_stream(stream);
+  const size_t kbytes = sizeof(_Float16) * (size_t)(rows_hi * kv_stride);
+  const size_t vbytes = sizeof(_Float16) * (size_t)((int64_t)n_kv_heads * head_dim * sp.vt_cols);
+  char* ws = nullptr;
+  const size_t total = 2 * kbytes + 2 * vbytes + 256;
+  OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), total, st), "hipMallocAsync(split)");
+  sp.kh = reinterpret_cast<_Float16*>(ws);
+  sp.kl = reinterpret_cast<_Float16*>(ws + kbytes);
+  sp.vh = reinterpret_cast<_Float16*>(ws + 2 * kbytes);
+  sp.vl = reinterpret_cast<_Float16*>(ws + 2 * kbytes + vbytes);
+  sp.overflow = reinterpret_cast<uint32_t*>(ws + 2 * kbytes + 2 * vbytes);
+  hipError_t e = hipMemsetAsync(sp.overflow, 0, sizeof(uint32_t), st);
+  if (e == hipSuccess) e = ovh::launch_attention_split(a, sp, max_rows, st);
+  uint32_t flag = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&flag, sp.overflow, sizeof flag, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFreeAsync(ws, st);
+  if (e != hipSuccess) return hip_fail(e, "attention_split");
+  if (flag)
+    return fail(OV_ERR_INVALID_ARG, "attention_split: |k| or |v| beyond the f16 range; use "
+                                    "ovh_attention");
   return OV_OK;
 }
 

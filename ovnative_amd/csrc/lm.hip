@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "../../include/ovnative_amd.h"
+#include "attn.h"
 #include "ovh_common.h"
 #include "status.h"
 
@@ -46,6 +47,7 @@ struct EmbTable {
   const float* f32;
   const int8_t* i8;
   const float* scale;
+  int64_t rows;
 };
 
 __device__ __forceinline__ float emb_at(const EmbTable& t, int64_t id, int64_t H, int64_t h) {
@@ -60,18 +62,21 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
   const int64_t row = blockIdx.x;
   const int64_t b = row / seq, s = row - b * seq;
   float* o = out + row * H;
+  // The host has range-checked every id; an id outside its table (which that
+  // check rules out) reads nothing and contributes zeros.
   if (mask[row]) {
     for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
       float acc = 0.f;
       for (int c = 0; c < C; ++c) {
         const int64_t id = ids[(b * C + c) * seq + s] + offsets[c];
-        acc = __fadd_rn(acc, emb_at(aud, id, H, h));
+        acc = __fadd_rn(acc, id >= 0 && id < aud.rows ? emb_at(aud, id, H, h) : 0.f);
       }
       o[h] = acc;
     }
   } else {
     const int64_t id = ids[b * C * seq + s];
-    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) o[h] = emb_at(tok, id, H, h);
+    const bool ok = id >= 0 && id < tok.rows;
+    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) o[h] = ok ? emb_at(tok, id, H, h) : 0.f;
   }
 }
 
@@ -131,8 +136,11 @@ __device__ float block_sum(float v, float* red) {
 __global__ __launch_bounds__(kSampleThreads) void guided_sample_kernel(
     const float* __restrict__ cond, int cond_seq, const float* __restrict__ uncond, int C, int V,
     int target_len, float guidance, float layer_penalty, int mask_id, int32_t* __restrict__ pred,
-    float* __restrict__ scores) {
+    float* __restrict__ scores, const uint32_t* __restrict__ flag_src,
+    uint32_t* __restrict__ flag_dst) {
   __shared__ float red[kSampleThreads / 64];
+  // the runner's overflow flag rides back with the results
+  if (blockIdx.x == 0 && threadIdx.x == 0) *flag_dst = *flag_src;
   __shared__ ArgMax ared[kSampleThreads / 64];
   const int idx = blockIdx.x;
   const int c = idx / target_len, t = idx - c * target_len;
@@ -245,9 +253,18 @@ struct OvhLm {
   float* logits = nullptr;
   bool device_sampling = false;
   std::vector<float> host_flat;
-  int32_t* d_pred = nullptr;
-  float* d_scores = nullptr;
+  // Pinned host staging: a forward's inputs go up in one copy (h_in, guarded by
+  // in_done so a copy in flight is never overwritten); a sample's results come
+  // back in one copy of d_out = [overflow flag | pad to 64 B][pred n][scores n].
+  char* h_in = nullptr;
+  size_t h_in_cap = 0;
+  hipEvent_t in_done = nullptr;
+  char* d_out = nullptr;
+  char* h_out = nullptr;
   int64_t sample_cap = 0;
+  // attention: split-f16 products (default) or fp32; overflow flag of the split
+  bool attn_split = true;
+  uint32_t* d_overflow = nullptr;
   // RoPE tables of the last position list (rebuilt only when it changes)
   std::vector<int64_t> tab_pos;
   std::vector<float> tab_host;
@@ -264,9 +281,13 @@ struct OvhLm {
     ovh_weight_free(head);
     for (void* p : allocs) (void)hipFree(p);
     if (arena) (void)hipFree(arena);
-    if (d_pred) (void)hipFree(d_pred);
-    if (d_scores) (void)hipFree(d_scores);
+    if (in_done) (void)hipEventSynchronize(in_done);
+    if (in_done) (void)hipEventDestroy(in_done);
+    if (h_in) (void)hipHostFree(h_in);
+    if (d_out) (void)hipFree(d_out);
+    if (h_out) (void)hipHostFree(h_out);
     if (d_tab) (void)hipFree(d_tab);
+    if (d_overflow) (void)hipFree(d_overflow);
   }
 };
 
@@ -338,7 +359,7 @@ int load_emb(OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t H
     return set_error(OV_ERR_INVALID_ARG, name + ": expected a row-major [rows, hidden] table");
   *rows = t->dims[0];
   void* d = nullptr;
-  *tab = ovh::EmbTable{nullptr, nullptr, nullptr};
+  *tab = ovh::EmbTable{nullptr, nullptr, nullptr, t->dims[0]};
   if (t->dtype == 0) {
     int rc = upload_bytes(L, t->data, sizeof(float) * (size_t)(t->dims[0] * H), &d);
     tab->f32 = static_cast<const float*>(d);
@@ -498,13 +519,17 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
       }
     }
   // Masks that are all ones add a zero bias: skip them.
-  std::vector<int64_t> bias_off(segs.size(), -1);
-  int64_t bias_elems = 0;
+  // The split attention takes masks as bit words, the fp32 kernel as biases.
+  const bool split = L.attn_split && (int)segs.size() <= ovh::kAttnMaxSegs;
+  std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
+  int64_t bias_elems = 0, bits_words = 0;
   for (size_t i = 0; i < segs.size(); ++i) {
     const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
     if (segs[i].mask && !all_ones(segs[i].mask, n)) {
       bias_off[i] = bias_elems;
       bias_elems += n;
+      bits_off[i] = bits_words;
+      bits_words += (int64_t)segs[i].rows * ((segs[i].rows + 31) / 32);
     }
   }
   const int64_t Kp_max = 32 * ovh::kb_of(I > QD ? (I > H ? I : H) : (QD > H ? QD : H));
@@ -518,14 +543,31 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     cur = align256(cur + bytes);
     return b;
   };
-  const Buf b_ids = take(sizeof(int64_t) * (size_t)(T * C)), b_am = take((size_t)T),
-            b_mask = take((size_t)bias_elems), b_bias = take(sizeof(float) * (size_t)bias_elems),
+  // inputs, contiguous for one upload: ids | audio mask | attention masks
+  const size_t ids_bytes = sizeof(int64_t) * (size_t)(T * C);
+  const size_t in_ids = 0, in_am = ids_bytes,                      // byte offsets
+               in_mask = in_am + (((size_t)T + 7) & ~(size_t)7),
+               in_bytes = in_mask + (size_t)bias_elems;
+  const Buf b_in = take(in_bytes),
+            b_bias = take(split ? 0 : sizeof(float) * (size_t)bias_elems),
+            b_bits = take(split ? sizeof(uint32_t) * (size_t)bits_words : 0),
             b_x = take(sizeof(float) * (size_t)(T * H)),
             b_aq = take((size_t)(T * Kp_max)), b_asc = take(sizeof(float) * (size_t)(T * Kb_max)),
             b_q = take(sizeof(float) * (size_t)(T * QD)), b_k = take(sizeof(float) * (size_t)(T * KVD)),
             b_v = take(sizeof(float) * (size_t)(T * KVD)), b_at = take(sizeof(float) * (size_t)(T * QD)),
             b_g = take(sizeof(float) * (size_t)(T * I)), b_u = take(sizeof(float) * (size_t)(T * I)),
             b_lg = take(sizeof(float) * (size_t)(T * CV));
+  // split-f16 attention planes (k rows as stored; V transposed, segments padded to 32)
+  int64_t vt_cols = 0;
+  std::vector<int64_t> vt_off(segs.size());
+  for (size_t i = 0; i < segs.size(); ++i) {
+    vt_off[i] = vt_cols;
+    vt_cols += (segs[i].rows + 31) / 32 * 32;
+  }
+  const Buf b_kh = take(split ? sizeof(_Float16) * (size_t)(T * KVD) : 0),
+            b_kl = take(split ? sizeof(_Float16) * (size_t)(T * KVD) : 0),
+            b_vh = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0),
+            b_vl = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0);
   if (cur > L.arena_cap) {
     if (L.arena) OVH_HIP(hipFree(L.arena), "hipFree(arena)");
     L.arena = nullptr;
@@ -535,8 +577,10 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     L.arena_cap = want;
   }
   auto at = [&](const Buf& b) { return static_cast<void*>(L.arena + b.off); };
-  int64_t* d_ids = static_cast<int64_t*>(at(b_ids));
-  uint8_t* d_am = static_cast<uint8_t*>(at(b_am));
+  char* d_in = static_cast<char*>(at(b_in));
+  int64_t* d_ids = reinterpret_cast<int64_t*>(d_in + in_ids);
+  uint8_t* d_am = reinterpret_cast<uint8_t*>(d_in + in_am);
+  uint8_t* d_mask = reinterpret_cast<uint8_t*>(d_in + in_mask);
   float* x = static_cast<float*>(at(b_x));
   int8_t* aq = static_cast<int8_t*>(at(b_aq));
   float* asc = static_cast<float*>(at(b_asc));
@@ -549,20 +593,44 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   float* logits = static_cast<float*>(at(b_lg));
   hipStream_t st = L.st;
 
-  OVH_HIP(hipMemcpyAsync(d_ids, ids, b_ids.bytes, hipMemcpyHostToDevice, st), "upload ids");
-  OVH_HIP(hipMemcpyAsync(d_am, audio_mask, b_am.bytes, hipMemcpyHostToDevice, st), "upload mask");
+  // stage the inputs in pinned memory (after the previous upload has left it)
+  if (!L.in_done) OVH_HIP(hipEventCreateWithFlags(&L.in_done, hipEventDisableTiming), "hipEventCreate");
+  OVH_HIP(hipEventSynchronize(L.in_done), "staging wait");
+  if (in_bytes > L.h_in_cap) {
+    if (L.h_in) OVH_HIP(hipHostFree(L.h_in), "hipHostFree(staging)");
+    L.h_in = nullptr;
+    L.h_in_cap = 0;
+    const size_t want = in_bytes + in_bytes / 4 + 4096;
+    OVH_HIP(hipHostMalloc(reinterpret_cast<void**>(&L.h_in), want, hipHostMallocDefault),
+            "hipHostMalloc(staging)");
+    L.h_in_cap = want;
+  }
+  std::memcpy(L.h_in + in_ids, ids, ids_bytes);
+  std::memcpy(L.h_in + in_am, audio_mask, (size_t)T);
+  for (size_t i = 0; i < segs.size(); ++i)
+    if (bias_off[i] >= 0)
+      std::memcpy(L.h_in + in_mask + bias_off[i], segs[i].mask,
+                  (size_t)segs[i].rows * (size_t)segs[i].rows);
+  OVH_HIP(hipMemcpyAsync(d_in, L.h_in, in_bytes, hipMemcpyHostToDevice, st), "upload inputs");
+  OVH_HIP(hipEventRecord(L.in_done, st), "hipEventRecord");
   std::vector<OvhAttnSegment> asegs(segs.size());
+  std::vector<const uint32_t*> seg_bits(segs.size(), nullptr);
   for (size_t i = 0; i < segs.size(); ++i) {
     const float* bias = nullptr;
     if (bias_off[i] >= 0) {
       const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
-      uint8_t* m = static_cast<uint8_t*>(at(b_mask)) + bias_off[i];
-      float* bb = static_cast<float*>(at(b_bias)) + bias_off[i];
-      OVH_HIP(hipMemcpyAsync(m, segs[i].mask, (size_t)n, hipMemcpyHostToDevice, st), "upload attn mask");
-      hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                         st, m, bb, n);
-      OVH_HIP(hipGetLastError(), "mask_to_bias launch");
-      bias = bb;
+      uint8_t* m = d_mask + bias_off[i];
+      if (split) {
+        uint32_t* bw = static_cast<uint32_t*>(at(b_bits)) + bits_off[i];
+        OVH_HIP(ovh::launch_mask_bits(m, segs[i].rows, bw, st), "mask_bits launch");
+        seg_bits[i] = bw;
+      } else {
+        float* bb = static_cast<float*>(at(b_bias)) + bias_off[i];
+        hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                           0, st, m, bb, n);
+        OVH_HIP(hipGetLastError(), "mask_to_bias launch");
+        bias = bb;
+      }
     }
     asegs[i] = OvhAttnSegment{bias, segs[i].rows, segs[i].row0 * QD, segs[i].row0 * KVD};
   }
@@ -574,6 +642,28 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   OVH_HIP(hipGetLastError(), "embed launch");
 
   const float scale = 1.f / std::sqrt((float)D);
+  ovh::AttnArgs aargs{};
+  ovh::AttnSplit sp{};
+  int max_rows = 0;
+  if (split) {
+    aargs.k = k; aargs.v = v; aargs.q = q; aargs.out = att;
+    aargs.q_stride = QD; aargs.kv_stride = KVD; aargs.out_stride = QD;
+    aargs.n_heads = c.n_heads; aargs.group = c.n_heads / c.n_kv_heads; aargs.scale = scale;
+    aargs.n_segs = (int)asegs.size();
+    for (size_t i = 0; i < asegs.size(); ++i) {
+      aargs.segs[i] = ovh::AttnSeg{nullptr, asegs[i].rows, asegs[i].q_off, asegs[i].kv_off,
+                                   seg_bits[i]};
+      sp.vt_off[i] = vt_off[i];
+      max_rows = asegs[i].rows > max_rows ? asegs[i].rows : max_rows;
+    }
+    sp.kh = static_cast<_Float16*>(at(b_kh));
+    sp.kl = static_cast<_Float16*>(at(b_kl));
+    sp.vh = static_cast<_Float16*>(at(b_vh));
+    sp.vl = static_cast<_Float16*>(at(b_vl));
+    sp.vt_cols = vt_cols;
+    sp.n_kv_heads = c.n_kv_heads;
+    sp.overflow = L.d_overflow;
+  }
   const int64_t qkv_n[3] = {QD, KVD, KVD};
   float* qkv_c[3] = {q, k, v};
   const int64_t gu_n[2] = {I, I};
@@ -581,12 +671,20 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   for (const OvhLm::Layer& Y : L.layers) {
     if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln1, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
     if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st)) != OV_OK) return rc;
-    if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb, sinb,
-                               c.rms_eps, st)) != OV_OK)
-      return rc;
-    if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
-                            QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
-      return rc;
+    if (split) {
+      // q/k norm + RoPE, f16 planes of k and V, then attention
+      OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
+                                             sinb, c.rms_eps, aargs, sp, max_rows, st),
+              "qk_norm_rope launch");
+      OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
+    } else {
+      if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb,
+                                 sinb, c.rms_eps, st)) != OV_OK)
+        return rc;
+      if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
+                              QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
+        return rc;
+    }
     if ((rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
     if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
     if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
@@ -598,6 +696,18 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   if ((rc = ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st)) != OV_OK) return rc;
   L.logits = logits;
   return OV_OK;
+}
+
+// The split attention reports |k| or |v| beyond the f16 range through a device
+// flag; checked (and cleared) wherever the runner synchronises with the host.
+int check_overflow(OvhLm& L) {
+  uint32_t flag = 0;
+  OVH_HIP(hipMemcpy(&flag, L.d_overflow, sizeof flag, hipMemcpyDeviceToHost), "read overflow flag");
+  if (!flag) return OV_OK;
+  const uint32_t zero = 0;
+  OVH_HIP(hipMemcpy(L.d_overflow, &zero, sizeof zero, hipMemcpyHostToDevice), "clear overflow flag");
+  return set_error(OV_ERR_INTERNAL, "attention inputs beyond the f16 range for the split-f16 "
+                                    "kernel: switch to ovh_lm_set_attention(lm, 0)");
 }
 
 bool config_ok(const OvhLmConfig& c) {
@@ -628,7 +738,11 @@ int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_te
   if (!L) return set_error(OV_ERR_INTERNAL, "out of host memory");
   L->cfg = *cfg;
   L->st = static_cast<hipStream_t>(stream);
-  const int rc = build(*L, ix);
+  int rc = OV_OK;
+  if (hipMalloc(reinterpret_cast<void**>(&L->d_overflow), sizeof(uint32_t)) != hipSuccess ||
+      hipMemset(L->d_overflow, 0, sizeof(uint32_t)) != hipSuccess)
+    rc = set_error(OV_ERR_INTERNAL, "hipMalloc(overflow flag)");
+  if (rc == OV_OK) rc = build(*L, ix);
   if (rc != OV_OK) {
     (void)hipStreamSynchronize(L->st);
     delete L;
@@ -665,6 +779,7 @@ int ovh_lm_forward(OvhLm* lm, int batch, int seq, const int64_t* input_ids,
                          hipMemcpyDeviceToHost, lm->st),
           "download logits");
   OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
+  if ((rc = check_overflow(*lm)) != OV_OK) return rc;
   for (int b = 0; b < batch; ++b)
     for (int cb = 0; cb < C; ++cb)
       for (int s = 0; s < seq; ++s)
@@ -691,13 +806,17 @@ int ovh_lm_forward_cfg(OvhLm* lm, int cond_seq, int uncond_seq, const int64_t* i
   OVH_HIP(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n, hipMemcpyDeviceToHost, lm->st),
           "download logits");
   OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
-  return OV_OK;
+  return check_overflow(*lm);
 }
 
 const void* ovh_lm_last_logits(const OvhLm* lm) { return lm ? lm->logits : nullptr; }
 
 void ovh_lm_set_device_sampling(OvhLm* lm, int on) {
   if (lm) lm->device_sampling = on != 0;
+}
+
+void ovh_lm_set_attention(OvhLm* lm, int split_f16) {
+  if (lm) lm->attn_split = split_f16 != 0;
 }
 
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,
@@ -709,30 +828,39 @@ int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond,
     return set_error(OV_ERR_INVALID_ARG, "sample: need 0 < target_len <= both plane lengths");
   const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab;
   const int64_t n = (int64_t)C * target_len;
+  constexpr size_t kHead = 64;  // overflow flag, padded
   if (n > lm->sample_cap) {
-    if (lm->d_pred) OVH_HIP(hipFree(lm->d_pred), "hipFree");
-    if (lm->d_scores) OVH_HIP(hipFree(lm->d_scores), "hipFree");
-    lm->d_pred = nullptr;
-    lm->d_scores = nullptr;
+    OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
+    if (lm->d_out) OVH_HIP(hipFree(lm->d_out), "hipFree");
+    if (lm->h_out) OVH_HIP(hipHostFree(lm->h_out), "hipHostFree");
+    lm->d_out = nullptr;
+    lm->h_out = nullptr;
     lm->sample_cap = 0;
-    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&lm->d_pred), sizeof(int32_t) * (size_t)n), "hipMalloc(pred)");
-    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&lm->d_scores), sizeof(float) * (size_t)n), "hipMalloc(scores)");
+    const size_t bytes = kHead + 8 * (size_t)n;
+    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&lm->d_out), bytes), "hipMalloc(sample out)");
+    OVH_HIP(hipHostMalloc(reinterpret_cast<void**>(&lm->h_out), bytes, hipHostMallocDefault),
+            "hipHostMalloc(sample out)");
     lm->sample_cap = n;
   }
+  const size_t bytes = kHead + 8 * (size_t)n;
+  int32_t* d_pred = reinterpret_cast<int32_t*>(lm->d_out + kHead);
+  float* d_scores = reinterpret_cast<float*>(lm->d_out + kHead + 4 * (size_t)n);
   // The mask token is the last audio id (kMaskId = 1024 with audio_vocab 1025,
   // cpp/src/model/tts.cpp:17).
   hipLaunchKernelGGL(ovh::guided_sample_kernel, dim3((unsigned)n), dim3(ovh::kSampleThreads), 0,
                      lm->st, static_cast<const float*>(cond), cond_seq,
                      static_cast<const float*>(uncond), C, V, target_len, guidance, layer_penalty,
-                     V - 1, lm->d_pred, lm->d_scores);
+                     V - 1, d_pred, d_scores, lm->d_overflow,
+                     reinterpret_cast<uint32_t*>(lm->d_out));
   OVH_HIP(hipGetLastError(), "guided sample launch");
-  OVH_HIP(hipMemcpyAsync(pred, lm->d_pred, sizeof(int32_t) * (size_t)n, hipMemcpyDeviceToHost, lm->st),
-          "download pred");
-  OVH_HIP(hipMemcpyAsync(scores, lm->d_scores, sizeof(float) * (size_t)n, hipMemcpyDeviceToHost,
-                         lm->st),
-          "download scores");
+  OVH_HIP(hipMemcpyAsync(lm->h_out, lm->d_out, bytes, hipMemcpyDeviceToHost, lm->st),
+          "download sample");
   OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
-  return OV_OK;
+  std::memcpy(pred, lm->h_out + kHead, 4 * (size_t)n);
+  std::memcpy(scores, lm->h_out + kHead + 4 * (size_t)n, 4 * (size_t)n);
+  uint32_t flag;
+  std::memcpy(&flag, lm->h_out, sizeof flag);
+  return flag ? check_overflow(*lm) : OV_OK;
 }
 
 

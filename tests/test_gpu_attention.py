@@ -125,6 +125,7 @@ def _segments(rng, seg_rows, masked):
     return segs, r0
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["fp32", "split_f16"])
 @pytest.mark.parametrize("seg_rows,nh,nkv,masked", [
     ([300, 300], 16, 8, False),   # BASELINE config 3/4: CFG batch 2, seq 300
     ([300, 260], 16, 8, True),    # ragged CFG (cond S, uncond T) with masks
@@ -132,7 +133,7 @@ def _segments(rng, seg_rows, masked):
     ([1, 33, 64, 65], 4, 2, True),
     ([7], 2, 2, False),
 ])
-def test_attention_vs_oracle(oracle, seg_rows, nh, nkv, masked):
+def test_attention_vs_oracle(oracle, seg_rows, nh, nkv, masked, split):
     import ovnative_amd as ov
     rng = np.random.default_rng(sum(seg_rows) + nh)
     D = 128
@@ -142,9 +143,10 @@ def test_attention_vs_oracle(oracle, seg_rows, nh, nkv, masked):
     v = rng.standard_normal((T, nkv * D)).astype(np.float32)
     want = oracle.attention(q, k, v, segs, nh, nkv, D)
     dsegs = [(None if b is None else dev(b), rows, r0, k0) for b, rows, r0, k0 in segs]
-    got = host(ov.attention(dev(q), dev(k), dev(v), dsegs, nh, nkv, D))
+    got = host(ov.attention(dev(q), dev(k), dev(v), dsegs, nh, nkv, D, split=split))
     err = _attn_err(got, want)
-    print(f"attention {seg_rows} nh={nh} nkv={nkv} masked={masked}: max err {err:.3g}")
+    print(f"attention {'split' if split else 'fp32'} {seg_rows} nh={nh} nkv={nkv} "
+          f"masked={masked}: max err {err:.3g}")
     assert err <= ATTN_TOL
     dead = np.all(want == 0, axis=1)
     assert np.all(got[dead] == 0)
@@ -165,3 +167,23 @@ def test_attention_sharp_and_argument_errors(oracle):
         ov.attention(dev(q[:, :64]), dev(k[:, :64]), dev(v[:, :64]), [(None, S, 0, 0)], 1, 1, 64)
     with pytest.raises(ov.InvalidArgument):
         ov.attention(dev(q), dev(k), dev(v), [(None, S, 0, 0)], 3, 2, D)
+
+
+def test_attention_split_golden_and_range(golden):
+    """The split-f16 form on the reference's golden cases, and its f16-range check."""
+    import ovnative_amd as ov
+    for c in _cases(golden, "attn"):
+        q, k, v = golden[c + "_q"], golden[c + "_k"], golden[c + "_v"]
+        S, D = q.shape
+        if D != 128:
+            continue
+        bias = dev(golden[c + "_bias"]) if int(golden[c + "_masked"]) else None
+        out = host(ov.attention(dev(q), dev(k), dev(v), [(bias, S, 0, 0)], 1, 1, 128,
+                                split=True))
+        assert _attn_err(out, golden[c + "_out"]) <= ATTN_TOL, c
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((16, 128)).astype(np.float32)
+    v = rng.standard_normal((16, 128)).astype(np.float32)
+    v[3, 7] = 1e5                                   # beyond f16
+    with pytest.raises(ov.InvalidArgument):
+        ov.attention(dev(q), dev(q), dev(v), [(None, 16, 0, 0)], 1, 1, 128, split=True)

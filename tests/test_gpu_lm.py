@@ -66,8 +66,9 @@ def small_lm():
     lm.close()
 
 
-def _device_attention(cfg):
-    """The HIP attention kernel as a drop-in for the oracle's attention step."""
+def _device_attention(cfg, split=True):
+    """The HIP attention kernel (the runner's default split-f16 form, or the fp32
+    form) as a drop-in for the oracle's attention step."""
     import ovnative_amd as ov
 
     def run(q, k, v, segs):
@@ -75,24 +76,29 @@ def _device_attention(cfg):
                  for b, r, r0, k0 in segs]
         out = ov.attention(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
                            torch.from_numpy(v).cuda(), dsegs, cfg["n_heads"],
-                           cfg["n_kv_heads"], cfg["head_dim"])
+                           cfg["n_kv_heads"], cfg["head_dim"], split=split)
         torch.cuda.synchronize()
         return out.cpu().numpy()
     return run
 
 
-def test_forward_bit_exact_given_attention(oracle, small_lm):
+@pytest.mark.parametrize("split", [True, False], ids=["split_f16", "fp32"])
+def test_forward_bit_exact_given_attention(oracle, small_lm, split):
     """Every step except attention is the reference's arithmetic bit for bit:
     with the device attention kernel substituted into the oracle's forward, the
-    runner's logits are identical."""
+    runner's logits are identical (both attention forms of the runner)."""
     ts, table, lm = small_lm
     ids, am, attn, pos = make_inputs(11, SMALL, 2, 70, 12)
-    got = lm.forward(ids, am, attn, pos)                  # [B, C, S, V]
+    lm.set_attention(split)
+    try:
+        got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
+    finally:
+        lm.set_attention(True)
     B, Cb, S, V = got.shape
     flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
     segs = [(attn[b], S, b * S) for b in range(B)]
     hybrid = oracle.lm_forward(SMALL, table, ids, am, segs, pos.reshape(-1),
-                               attention=_device_attention(SMALL))
+                               attention=_device_attention(SMALL, split))
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
