@@ -476,7 +476,8 @@ constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kMaskedLog2 = -1e29f * kLog2e;
 
 template <bool kBits>
-__global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, AttnSplit sp) {
+__global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, AttnSplit sp,
+                                                                 int qtiles, int per_xcd) {
   // The Q planes (2 x 32 x kQPad halves) alias the start of `part`, which is
   // written only after every wavefront has left the key loop.
   __shared__ __attribute__((aligned(16))) float part[kAttnWaves][kAttnQ][kAttnD];
@@ -485,11 +486,20 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   _Float16* qs_h = reinterpret_cast<_Float16*>(&part[0][0][0]);
   _Float16* qs_l = qs_h + kAttnQ * kQPad;
 
-  const AttnSeg seg = args.segs[blockIdx.z];
+  // XCD-aware task order: workgroups reach the 8 XCDs round-robin (id % 8);
+  // XCD x takes the x-th contiguous range of tasks, and tasks are numbered
+  // (segment, KV head, head in group, query tile)-major, so the two heads of a
+  // KV group and all their query tiles read K/V planes held in one L2.
+  const int task = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (task >= args.n_segs * args.n_heads * qtiles) return;
+  const int qt = task % qtiles;
+  const int sh = task / qtiles;  // segment * n_heads + head; heads of a KV group adjacent
+  const int sidx = sh / args.n_heads;
+  const int h = sh - sidx * args.n_heads, kvh = h / args.group;
+  const AttnSeg seg = args.segs[sidx];
   const int S = seg.rows;
-  const int q0 = blockIdx.x * kAttnQ;
+  const int q0 = qt * kAttnQ;
   if (q0 >= S) return;
-  const int h = blockIdx.y, kvh = h / args.group;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
 
@@ -522,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   const int64_t krow0 = seg.kv_off / args.kv_stride;  // segment's first k row
   const _Float16* __restrict__ khb = sp.kh + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
   const _Float16* __restrict__ klb = sp.kl + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
-  const int64_t vbase = (int64_t)kvh * kAttnD * sp.vt_cols + sp.vt_off[blockIdx.z];
+  const int64_t vbase = (int64_t)kvh * kAttnD * sp.vt_cols + sp.vt_off[sidx];
   const _Float16* __restrict__ vhb = sp.vh + vbase;
   const _Float16* __restrict__ vlb = sp.vl + vbase;
   const uint32_t vlane = (uint32_t)(r32 * sp.vt_cols + 8 * hf);
@@ -765,12 +775,17 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   if ((uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
       (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((max_rows + kAttnQ - 1) / kAttnQ), (unsigned)args.n_heads,
-                  (unsigned)args.n_segs);
+  // 1-D grid of 8 * per_xcd workgroups (XCD-aware task order in the kernel)
+  const int qtiles = (max_rows + kAttnQ - 1) / kAttnQ;
+  const int tasks = args.n_segs * args.n_heads * qtiles;
+  const int per_xcd = (tasks + 7) / 8;
+  const dim3 grid((unsigned)(8 * per_xcd));
   if (mask_bits)
-    hipLaunchKernelGGL(attention_split_kernel<true>, grid, dim3(256), 0, st, args, sp);
+    hipLaunchKernelGGL(attention_split_kernel<true>, grid, dim3(256), 0, st, args, sp, qtiles,
+                       per_xcd);
   else
-    hipLaunchKernelGGL(attention_split_kernel<false>, grid, dim3(256), 0, st, args, sp);
+    hipLaunchKernelGGL(attention_split_kernel<false>, grid, dim3(256), 0, st, args, sp, qtiles,
+                       per_xcd);
   return hipGetLastError();
 }
 

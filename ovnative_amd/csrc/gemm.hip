@@ -292,6 +292,226 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-tile variant: 16x16 wave tiles on V_MFMA_I32_16X16X32_I8 (again one
+// 32-k block per instruction; a lane holds 4 accumulators of one activation
+// row, D[4*(l/16) + e][l%16]), operands moved global -> LDS by the DMA path
+// (global_load_lds_dwordx4: lane l's 16 bytes land at the stage address +
+// 16 l, i.e. block tiles in the same lane order as above) and the activation
+// scales with them, through a two-stage LDS ring.  No staging registers and
+// small accumulator sets leave room for many wavefronts per SIMD, which is what
+// hides the LDS and memory latency behind the VALU epilogue here; the 16-row
+// tiles give narrow-N shapes (N = 1024) several times more wavefronts.
+// Fragment of a 16-row tile (rows 16h..16h+15 of a 32-row block tile): lane l
+// reads 8 bytes of row 16h + l%16 at k = 8*(l/16): chunk (l/32)*32 + row, byte
+// 8*((l/16) & 1) of that 16-byte chunk.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ i32x4 mfma16_i8(int64_t a, int64_t b) {
+  const i32x4 z = {0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone): this
+// wavefront's DMA ops older than the last N have landed in LDS and its own LDS
+// reads have returned.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.
+template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE>
+__global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) {
+  constexpr int NW = WN * WM;
+  constexpr int TN = BN / WN, TM = BM / WM;
+  constexpr int FN = TN / 16, FM = TM / 16;
+  static_assert(FN >= 1 && FM >= 1 && TN % 16 == 0 && TM % 16 == 0, "16-row wave tiles");
+  static_assert(BN % 32 == 0 && BM % 32 == 0 && BM <= 64, "32-row block tiles; one scale row per lane");
+  static_assert(SB % 4 == 0 && NST >= 2, "scales move in 16-byte (4-block) chunks");
+  constexpr int WT = BN / 32, AT = BM / 32;
+  constexpr int TILES = (WT + AT) * SB;   // 1 KiB block tiles per stage
+  constexpr int SCL = TILES * TILE;       // stage offset of the scales: [SB/4][BM rows][4 floats]
+  constexpr int STAGE = SCL + BM * SB * 4;
+  constexpr int TPW = (TILES + NW - 1) / NW;
+  constexpr bool EVEN = TILES % NW == 0;
+  __shared__ __attribute__((aligned(16))) int8_t smem[NST][STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave % WN, wm = wave / WN;
+  const int n_tiles = (a.N + BN - 1) / BN;
+  int ntile, mtile;
+  if (!tile_of(blockIdx.x, n_tiles, ntile, mtile)) return;  // padding workgroup
+  const int n0 = ntile * BN, m0 = mtile * BM;
+  const int Kb = a.Kb;
+  const int64_t Kp = a.Kp;
+  const int nstages = Kb / SB;
+
+  // DMA slots of this wavefront: stage tile idx = r * SB + bb (r < WT: weight
+  // row tile, else activation row tile), wavefront w takes idx = w, w + NW, ...
+  const int8_t* src[TPW];
+  int64_t step[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    int idx = wave + t * NW;
+    idx = idx < TILES ? idx : TILES - 1;
+    const int bb = idx % SB, r = idx / SB;
+    if (r < WT) {
+      src[t] = a.W + ((int64_t)(n0 / 32 + r) * Kb + bb) * TILE + lane * 16;
+      step[t] = (int64_t)SB * TILE;
+    } else {
+      int row = m0 + (r - WT) * 32 + (lane & 31);
+      row = row < a.M ? row : a.M - 1;  // rows are independent: clamp, discard later
+      src[t] = a.aq + (int64_t)row * Kp + bb * 32 + (lane >> 5) * 16;
+      step[t] = SB * 32;
+    }
+  }
+  const float* ssrc;
+  {
+    int row = m0 + lane;
+    row = row < a.M ? row : a.M - 1;
+    ssrc = a.asc + (int64_t)row * Kb;
+  }
+  // Stage s -> ring slot s % NST.  The last wavefront also moves the scales
+  // (SB/4 more DMA ops); a wavefront's DMA ops complete in issue order.
+  auto issue = [&](int s) __attribute__((always_inline)) {
+    int8_t* base = smem[s % NST];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int idx = wave + t * NW;
+      if (EVEN || idx < TILES)  // uniform for the wavefront
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[t] + s * step[t]),
+                                         (lds_void_t*)(base + idx * TILE), 16, 0, 0);
+    }
+    if (wave == NW - 1 && lane < BM) {
+#pragma unroll
+      for (int c = 0; c < SB / 4; ++c)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc + s * SB + 4 * c),
+                                         (lds_void_t*)(base + SCL + c * BM * 16), 16, 0, 0);
+    }
+  };
+  // Waiting for stage s: the DMA ops issued after it (stages s+1 .. s+NST-2)
+  // may stay in flight.  TPW per stage is the fewest any wavefront issues, so
+  // the count is conservative for the wavefront that also moves the scales.
+  constexpr int LATER = (EVEN ? TPW : TPW - 1) * (NST - 2);
+  // fragment byte offsets inside a block tile (see above)
+  const int q = lane >> 4;
+  const int frag = ((q >> 1) * 32 + (lane & 15)) * 16 + (q & 1) * 8;
+  int aoff[FN], boff[FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+    const int t16 = wn * FN + i;
+    aoff[i] = (t16 >> 1) * SB * TILE + (t16 & 1) * 16 * 16 + frag;
+  }
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int t16 = wm * FM + j;
+    boff[j] = (WT + (t16 >> 1)) * SB * TILE + (t16 & 1) * 16 * 16 + frag;
+  }
+
+  f32x4 f[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) f[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nstages) issue(s);
+  for (int s = 0; s < nstages; ++s) {
+    if (s + NST - 2 < nstages)
+      wait_vm_lgkm<LATER>();  // this wavefront's DMA for stage s landed
+    else
+      wait_vm_lgkm<0>();
+    // ... and every other wavefront's.  A bare s_barrier: __syncthreads()'s
+    // release fence would also drain the later stages' DMA (vmcnt(0)).
+    __builtin_amdgcn_s_barrier();
+    // slot (s + NST - 1) % NST was read in iteration s - 1, which every
+    // wavefront has left
+    if (s + NST - 1 < nstages) issue(s + NST - 1);
+    const int8_t* base = smem[s % NST];
+    f32x4 sc[SB / 4][FM];
+#pragma unroll
+    for (int c = 0; c < SB / 4; ++c)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        sc[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
+                                                   (wm * TM + 16 * j + (lane & 15)) * 16);
+#pragma unroll
+    for (int bb = 0; bb < SB; ++bb) {
+      int64_t af[FN], bf[FM];
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        af[i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        bf[j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const i32x4 acc = mfma16_i8(af[i], bf[j]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            f[i][j][e] = fmaf((float)acc[e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+        }
+    }
+  }
+
+  // column scale, optional residual add, slice-aware store: lane holds
+  // n = tile + 4*(l/16) + e (4 consecutive columns) of row m = tile + l%16
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int nb = n0 + (wn * FN + i) * 16 + 4 * q;
+      if (nb >= a.N) continue;
+      const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + nb);
+      int s = 0;
+#pragma unroll
+      for (int t = 1; t < kMaxSlices; ++t)
+        if (t < a.nslices && nb >= a.start[t]) s = t;
+      float* dst = a.out[s] + (int64_t)m * a.ld[s] + (nb - a.start[s]);
+      const int lim = a.start[s + 1] - nb;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(f[i][j][e], ws[e]);
+      if (lim >= 4 && ((uintptr_t)dst & 15u) == 0) {
+        f32x4 v;
+        if (MODE == kAccumulate) {
+          const f32x4 c = *reinterpret_cast<const f32x4*>(dst);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(o[e], c[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = o[e];
+        }
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (e < lim) dst[e] = MODE == kAccumulate ? __fadd_rn(o[e], dst[e]) : o[e];
+      }
+    }
+  }
+}
+
+// Launchable when Kb % SB == 0.
+template <int BN, int BM, int WN, int WM, int SB, int NST>
+hipError_t launch_cfg16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
+  if (a.Kb % SB) return hipErrorInvalidValue;
+  const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
+  if (mode == kAccumulate)
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumulate>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kStore>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 template <int BN, int BM, int WN, int WM, int SB>
 hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
@@ -327,6 +547,15 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // MFMAs), mid-size ones 64x64, and skinny M or N = 1024 one-wave 32x32 tiles,
   // which give the most wavefronts for the few output tiles there are.
   const int64_t M = a.M, N = a.N;
+  if (mode != kDumpBlocks && a.Kb % 4 == 0) {
+    // 16x16 wave tiles (sweep on MI355X, LM shapes at M = 128 / 600 / 16384):
+    // many small workgroups for the skinny and N = 1024 shapes, 128x64 tiles
+    // of 8 wavefronts for wide N at M >= 512.
+    if (M >= 2048) return launch_cfg16<128, 64, 4, 2, 4, 3>(a, mode, st);
+    if (M >= 512 && N >= 6144) return launch_cfg16<128, 64, 4, 2, 4, 2>(a, mode, st);
+    if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2>(a, mode, st);
+    return launch_cfg16<32, 32, 2, 2, 4, 2>(a, mode, st);
+  }
   if (M >= 2048 || (M >= 512 && N >= 6144)) return launch_cfg<128, 64, 2, 2>(a, mode, st);
   if (M >= 256) return launch_cfg<64, 64, 2, 2>(a, mode, st);
   return launch_cfg<32, 32, 1, 1>(a, mode, st);

@@ -19,5 +19,16 @@ extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const 
     case 6: return launch_cfg<64, 32, 2, 1>(a, mode, s);
     case 7: return launch_cfg<32, 32, 1, 1>(a, mode, s);
   }
+  if (Kb % 4) return -1;  // 16x16 variants: 4- or 8-block stages only
+  switch (cfg) {
+    case 8: return launch_cfg16<32, 32, 2, 2, 4, 2>(a, mode, s);
+    case 9: return launch_cfg16<64, 32, 4, 1, 4, 2>(a, mode, s);
+    case 10: return launch_cfg16<128, 64, 4, 2, 4, 2>(a, mode, s);
+    case 11: return launch_cfg16<128, 64, 4, 2, 4, 3>(a, mode, s);
+    case 12: return launch_cfg16<64, 32, 4, 2, 4, 2>(a, mode, s);
+    case 13: return launch_cfg16<64, 64, 2, 2, 4, 3>(a, mode, s);
+    case 14: return launch_cfg16<32, 32, 2, 2, 8, 2>(a, mode, s);
+    case 15: return launch_cfg16<64, 32, 2, 2, 4, 3>(a, mode, s);
+  }
   return -1;
 }

@@ -12,7 +12,13 @@ lib = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libgemm_t
 lib.tune_gemm.argtypes = [C.c_int]*4 + [C.c_void_p]*5 + [C.c_int, C.c_void_p]
 class DW(C.Structure):
     _fields_ = [('N', C.c_int64), ('K', C.c_int64), ('Npad', C.c_int64), ('Kb', C.c_int64), ('Kp', C.c_int64), ('q', C.c_void_p), ('scale', C.c_void_p)]
-cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x128', 6: '64x32', 7: '32x32'}
+# 0-7: the 32x32-tile kernel (register-staged); 8-15: the 16x16-tile kernel
+# (LDS DMA ring): s<BN>x<BM>w<waves>[b<blocks per stage>][n<ring stages>]
+cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x128', 6: '64x32', 7: '32x32',
+        8: 's32x32w4', 9: 's64x32w4', 10: 's128x64w8', 11: 's128x64w8n3', 12: 's64x32w8',
+        13: 's64x64w4n3', 14: 's32x32w4b8', 15: 's64x32w4xn3'}
+if len(sys.argv) > 1:
+    cfgs = {k: v for k, v in cfgs.items() if str(k) in sys.argv[1].split(',')}
 shapes = [(600, 6144, 1024), (600, 4096, 1024), (600, 1024, 2048), (600, 1024, 3072), (600, 8192, 1024),
           (128, 4096, 1024), (128, 6144, 1024), (128, 1024, 2048), (128, 1024, 3072), (128, 2048, 1024), (128, 1024, 1024),
           (256, 3072, 1024), (16384, 6144, 1024), (16384, 1024, 3072)]
