@@ -61,6 +61,11 @@ struct AttnSplit {
   int64_t vt_off[kAttnMaxSegs];
   int32_t n_kv_heads;
   uint32_t* overflow;  // set non-zero when a |k| or |v| is beyond the f16 range
+  // Optional: the output quantised per 32-column block as s8_nk_quantize does
+  // (codes [rows][out_stride], scales [rows][out_stride / 32]) instead of the
+  // fp32 `out`; needs q_stride == out_stride and segment q offsets in whole rows.
+  int8_t* aq;
+  float* asc;
 };
 // Splits K (the rows the segments cover) and V into the planes, then attends.
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,

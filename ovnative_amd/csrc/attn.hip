@@ -712,37 +712,66 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     lstat[wave][r32] = l_run;
   }
   __syncthreads();
+  // 8 threads per query row, 16 columns each (a 32-column block = a lane pair)
   const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
-  if (q0 + qi >= S) return;
+  const bool valid = q0 + qi < S;  // the pair exchange below needs both lanes
   float M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mstat[w][qi]);
-  float* dst = args.out + seg.q_off + (int64_t)(q0 + qi) * args.out_stride + (int64_t)h * kAttnD + d0;
+  float ov[16];
   if (M < kMaskedLog2) {  // fully masked row (largest biased score below -1e29)
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) *reinterpret_cast<f32x4*>(dst + j) = f32x4{0.f, 0.f, 0.f, 0.f};
-    return;
-  }
-  float f[kAttnWaves], L = 0.f;
-#pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) {
-    f[w] = mstat[w][qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mstat[w][qi] - M);
-    L = fmaf(lstat[w][qi], f[w], L);
-  }
-  const float inv = __fdiv_rn(1.f, L);
-#pragma unroll
-  for (int j = 0; j < 16; j += 4) {
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 16; ++j) ov[j] = 0.f;
+  } else {
+    float f[kAttnWaves], L = 0.f;
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(&part[w][qi][d0 + j]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[c] = fmaf(x[c], f[w], acc[c]);
+      f[w] = mstat[w][qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mstat[w][qi] - M);
+      L = fmaf(lstat[w][qi], f[w], L);
     }
+    const float inv = __fdiv_rn(1.f, L);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = __fmul_rn(acc[c], inv);
-    *reinterpret_cast<f32x4*>(dst + j) = acc;
+    for (int j = 0; j < 16; j += 4) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(&part[w][qi][d0 + j]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = fmaf(x[c], f[w], acc[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ov[j + c] = __fmul_rn(acc[c], inv);
+    }
   }
+  if (sp.aq) {
+    const int64_t row = seg.q_off / args.q_stride + q0 + qi;
+    // s8_nk_quantize of this 32-column block: amax over the lane pair, then
+    // the same scale and rounding as quantize_kernel (quant_block_lane).
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(ov[j]));
+    const float amax = fmaxf(a, __shfl_xor(a, 1));
+    const float qinv = amax > 0.f ? __fdiv_rn(127.0f, amax) : 0.f;
+    i32x4 codes;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        packed |= (uint32_t)(uint8_t)(int8_t)quant_q(ov[4 * c + e], qinv) << (8 * e);
+      codes[c] = (int)packed;
+    }
+    if (!valid) return;
+    const int64_t col = (int64_t)h * kAttnD + d0;
+    *reinterpret_cast<i32x4*>(sp.aq + row * args.out_stride + col) = codes;
+    if ((threadIdx.x & 1) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(amax, 127.0f);
+    return;
+  }
+  if (!valid) return;
+  float* dst = args.out + seg.q_off + (int64_t)(q0 + qi) * args.out_stride + (int64_t)h * kAttnD + d0;
+#pragma unroll
+  for (int j = 0; j < 16; j += 4)
+    *reinterpret_cast<f32x4*>(dst + j) = f32x4{ov[j], ov[j + 1], ov[j + 2], ov[j + 3]};
 }
 
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
@@ -771,6 +800,12 @@ hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int
 hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                        bool mask_bits, hipStream_t st) {
   if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
+  if (sp.aq) {  // quantised output: whole rows of one stride, 32-column blocks
+    if (args.q_stride != args.out_stride || args.out_stride % 32 != 0 || !sp.asc)
+      return hipErrorInvalidValue;
+    for (int i = 0; i < args.n_segs; ++i)
+      if (args.segs[i].q_off % args.q_stride != 0) return hipErrorInvalidValue;
+  }
   // per-lane plane offsets are 32-bit
   if ((uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
       (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))

@@ -663,6 +663,8 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     sp.vt_cols = vt_cols;
     sp.n_kv_heads = c.n_kv_heads;
     sp.overflow = L.d_overflow;
+    sp.aq = aq;  // attention writes the o_proj input already quantised
+    sp.asc = asc;
   }
   const int64_t qkv_n[3] = {QD, KVD, KVD};
   float* qkv_c[3] = {q, k, v};
@@ -685,7 +687,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
                               QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
         return rc;
     }
-    if ((rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
+    if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
     if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
     if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
     if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
