@@ -349,8 +349,8 @@ def main():
         "config": {
             "workload": (f"one CFG decoding step of the {args.layers}-layer LM: forward at B=2, "
                          f"S={SEQ} ({TEXT} text + {SEQ - TEXT} audio; uncond = target slice), "
-                         "int8-nk linears, fp32 GQA attention, head 1024->8x1025, device guided "
-                         "sampling"),
+                         "int8-nk linears, GQA attention (split-f16 matrix-core products, fp32 "
+                         "softmax), head 1024->8x1025, device guided sampling"),
             "model": "Qwen3-0.6B-shaped LM (hidden 1024, 16/8 heads x 128, inter 3072, 28 layers)",
             "global_batch": CFG_BATCH,
             "seq_len": SEQ,
@@ -362,7 +362,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_i8 gate/up merged (M=600, N=6144, K=1024)",
+            "kernel": "gemm16 gate/up merged (M=600, N=6144, K=1024)",
             "achieved": round(gu_tops, 2),
             "peak": PEAK_INT8_TOPS,
             "unit": "TFLOP/s",

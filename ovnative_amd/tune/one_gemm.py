@@ -2,7 +2,8 @@
 
     python3 ovnative_amd/tune/one_gemm.py CFG M N K REPS
 
-CFG indexes the configs of gemm_tune.hip (4 = 128x64, 2 = 64x64, 7 = 32x32)."""
+CFG indexes the configs of gemm_tune.hip (4 = 128x64, 2 = 64x64, 7 = 32x32;
+10 = the 16x16-tile 128x64 x 8-wave kernel the product uses for gate/up at M = 600)."""
 import ctypes as C, sys, os
 sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
 import torch, ovnative_amd as ov
