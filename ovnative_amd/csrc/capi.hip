@@ -16,10 +16,8 @@
 #include "ovh_common.h"
 #include "quant.h"
 #include "status.h"
+#include "weight.h"
 
-struct OvhWeight {
-  ovh::DeviceWeight w;
-};
 
 namespace {
 thread_local std::string t_err;
@@ -86,6 +84,25 @@ ovh::GemmArgs base_args(int64_t M, const int8_t* aq, const float* asc, const Ovh
 }
 
 }  // namespace
+
+namespace ovh {
+int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
+                        OvhWeight** out) {
+  *out = nullptr;
+  if (!gate || !up || gate->w.N != up->w.N || gate->w.K != up->w.K || gate->w.N % 64 != 0)
+    return fail(OV_ERR_INVALID_ARG, "interleave: gate/up need equal shapes, rows a multiple of 64");
+  OvhWeight* h = nullptr;
+  const int rc = new_weight(2 * gate->w.N, gate->w.K, &h);
+  if (rc != OV_OK) return rc;
+  const hipError_t e = launch_weight_interleave16(gate->w, up->w, h->w, st);
+  if (e != hipSuccess) {
+    ovh_weight_free(h);
+    return hip_fail(e, "weight interleave");
+  }
+  *out = h;
+  return OV_OK;
+}
+}  // namespace ovh
 
 extern "C" {
 

@@ -11,7 +11,7 @@ constexpr int kMaxSlices = 8;
 // N-tile the kernels use (32..128 rows) reads in-bounds rows and zero scales.
 constexpr int kRowPad = 128;
 
-enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2 };
+enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2, kSiluQuant = 3 };
 
 // Device weight: int8 [Npad][Kp] row-major (row n = output channel n, K tail
 // and rows >= N zero) and fp32 scale [Npad] (0 beyond N).
@@ -33,11 +33,19 @@ struct GemmArgs {
   float* out[kMaxSlices] = {nullptr};
   int64_t ld[kMaxSlices] = {0};
   int32_t* dump = nullptr;      // [M][N][Kb] in kDumpBlocks mode
+  // kSiluQuant (W interleaved by weight_interleave16, N = 2I, I % 64 == 0):
+  // h = silu(gate) * up quantised per 32-column block as silu_mul_quantize
+  // does, codes [M][hKp] and scales [M][hKp / 32]; `out` is unused.
+  int8_t* hq = nullptr;
+  float* hsc = nullptr;
+  int64_t hKp = 0;
 };
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
                                 const float* scale_src, DeviceWeight& dst, hipStream_t st);
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st);
+hipError_t launch_weight_interleave16(const DeviceWeight& gate, const DeviceWeight& up,
+                                      DeviceWeight& dst, hipStream_t st);
 
 }  // namespace ovh

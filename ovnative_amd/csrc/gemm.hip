@@ -459,6 +459,54 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     }
   }
 
+  if constexpr (MODE == kSiluQuant) {
+    // Tiles 4p..4p+3 of the wavefront are gate, up, gate, up rows of 32
+    // consecutive h columns (weight_interleave16): lane holds g and u of
+    // h columns c0 + 4q + e and c0 + 16 + 4q + e of row m.  The gate and up
+    // values are the fp32 outputs the sliced store would write (f * wscale);
+    // the block amax spans the 4 lanes of row m (l, l^16, l^32, l^48).
+    static_assert(FN % 4 == 0, "a wavefront covers whole 32-column blocks of h");
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
+#pragma unroll
+      for (int pb = 0; pb < FN / 4; ++pb) {
+        const int t = 4 * pb;
+        const int nr = n0 + (wn * FN + t) * 16 + 4 * q;  // merged row of gate value e = 0
+        const f32x4 wg0 = *reinterpret_cast<const f32x4*>(a.ws + nr);
+        const f32x4 wu0 = *reinterpret_cast<const f32x4*>(a.ws + nr + 16);
+        const f32x4 wg1 = *reinterpret_cast<const f32x4*>(a.ws + nr + 32);
+        const f32x4 wu1 = *reinterpret_cast<const f32x4*>(a.ws + nr + 48);
+        float h[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          h[e] = silu_up_lane(__fmul_rn(f[t][j][e], wg0[e]), __fmul_rn(f[t + 1][j][e], wu0[e]));
+          h[4 + e] =
+              silu_up_lane(__fmul_rn(f[t + 2][j][e], wg1[e]), __fmul_rn(f[t + 3][j][e], wu1[e]));
+        }
+        float am = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(h[e]));
+        am = fmaxf(am, __shfl_xor(am, 16));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        const float qinv = am > 0.f ? __fdiv_rn(127.0f, am) : 0.f;
+        uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          c0 |= (uint32_t)(uint8_t)(int8_t)quant_q(h[e], qinv) << (8 * e);
+          c1 |= (uint32_t)(uint8_t)(int8_t)quant_q(h[4 + e], qinv) << (8 * e);
+        }
+        if (m >= a.M) continue;
+        const int64_t col = (int64_t)((n0 + (wn * FN + t) * 16) / 32) * 16;  // h column of the block
+        int8_t* dst = a.hq + (int64_t)m * a.hKp + col + 4 * q;
+        *reinterpret_cast<uint32_t*>(dst) = c0;
+        *reinterpret_cast<uint32_t*>(dst + 16) = c1;
+        if (q == 0) a.hsc[(int64_t)m * (a.hKp / 32) + col / 32] = __fdiv_rn(am, 127.0f);
+      }
+    }
+    return;
+  }
+
   // column scale, optional residual add, slice-aware store: lane holds
   // n = tile + 4*(l/16) + e (4 consecutive columns) of row m = tile + l%16
 #pragma unroll
@@ -512,6 +560,17 @@ hipError_t launch_cfg16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The SiLU-fused mode (wave tiles 64 rows wide: BN / WN == 64).
+template <int BN, int BM, int WN, int WM, int SB, int NST>
+hipError_t launch_cfg16_silu(const GemmArgs& a, hipStream_t st) {
+  static_assert(BN / WN == 64, "four 16-row tiles per wavefront");
+  if (a.Kb % SB || a.N % 128 || !a.hq || !a.hsc || a.hKp < a.N / 2) return hipErrorInvalidValue;
+  const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
+  hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kSiluQuant>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 template <int BN, int BM, int WN, int WM, int SB>
 hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
@@ -547,6 +606,10 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // MFMAs), mid-size ones 64x64, and skinny M or N = 1024 one-wave 32x32 tiles,
   // which give the most wavefronts for the few output tiles there are.
   const int64_t M = a.M, N = a.N;
+  if (mode == kSiluQuant) {
+    if (a.Kb % 4) return hipErrorInvalidValue;
+    return launch_cfg16_silu<128, 64, 2, 2, 4, 2>(a, st);
+  }
   if (mode != kDumpBlocks && a.Kb % 4 == 0) {
     // 16x16 wave tiles (sweep on MI355X, LM shapes at M = 128 / 600 / 16384):
     // many small workgroups for the skinny and N = 1024 shapes, 128x64 tiles
@@ -613,6 +676,38 @@ hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int lay
   hipLaunchKernelGGL(scale_pad_kernel, dim3((unsigned)((w.Npad + 255) / 256)), dim3(256), 0, st,
                      N, w.Npad, scale_src, w.scale);
   return hipGetLastError();
+}
+
+// Block tile c of dst (rows 32c..32c+31) = gate rows 16c..16c+15, then up rows
+// 16c..16c+15; one thread per 16-byte chunk (chunk l of a tile = row l%32,
+// k 16*(l/32)..+15).  Load-time only.
+__global__ void weight_interleave16_kernel(int64_t I, int64_t Kb, const int8_t* __restrict__ g,
+                                           const int8_t* __restrict__ u, const float* __restrict__ gs,
+                                           const float* __restrict__ us, int8_t* __restrict__ dst,
+                                           float* __restrict__ ds) {
+  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = 2 * I / 32 * Kb * 64;
+  if (chunk >= total) return;
+  const int lane = (int)(chunk & 63);
+  const int64_t tile = chunk >> 6;
+  const int64_t c = tile / Kb, b = tile - c * Kb;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t srow = 16 * c + (r & 15);  // row of gate (r < 16) or up
+  const int8_t* src = (r < 16 ? g : u) + (((srow >> 5) * Kb + b) * 64 + (srow & 31) + 32 * h) * 16;
+  *reinterpret_cast<i32x4*>(dst + chunk * 16) = *reinterpret_cast<const i32x4*>(src);
+  if (b == 0 && h == 0) ds[32 * c + r] = (r < 16 ? gs : us)[srow];
+}
+
+hipError_t launch_weight_interleave16(const DeviceWeight& gate, const DeviceWeight& up,
+                                      DeviceWeight& dst, hipStream_t st) {
+  const int64_t chunks = 2 * gate.N / 32 * gate.Kb * 64;
+  hipLaunchKernelGGL(weight_interleave16_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256),
+                     0, st, gate.N, gate.Kb, gate.q, up.q, gate.scale, up.scale, dst.q, dst.scale);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || dst.Npad == 2 * gate.N) return e;
+  e = hipMemsetAsync(dst.q + 2 * gate.N * dst.Kp, 0, (size_t)((dst.Npad - 2 * gate.N) * dst.Kp), st);
+  if (e != hipSuccess) return e;
+  return hipMemsetAsync(dst.scale + 2 * gate.N, 0, sizeof(float) * (size_t)(dst.Npad - 2 * gate.N), st);
 }
 
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st) {

@@ -34,6 +34,7 @@
 #include "attn.h"
 #include "ovh_common.h"
 #include "status.h"
+#include "weight.h"
 
 namespace ovh {
 
@@ -262,6 +263,8 @@ struct OvhLm {
   char* d_out = nullptr;
   char* h_out = nullptr;
   int64_t sample_cap = 0;
+  // gate/up GEMM with silu(gate)*up quantised in its epilogue (inter % 64 == 0)
+  bool silu_fused = false;
   // attention: split-f16 products (default) or fp32; overflow flag of the split
   bool attn_split = true;
   uint32_t* d_overflow = nullptr;
@@ -421,8 +424,12 @@ int build(OvhLm& L, const TensorIndex& ix) {
       rc = ovh_weight_concat(parts, 3, L.st, &Y.qkv);
     }
     if (rc == OV_OK) {
-      const OvhWeight* parts[2] = {g, u};
-      rc = ovh_weight_concat(parts, 2, L.st, &Y.gate_up);
+      if (L.silu_fused) {  // rows interleaved for the SiLU-fused GEMM epilogue
+        rc = ovh::weight_interleave16(g, u, L.st, &Y.gate_up);
+      } else {
+        const OvhWeight* parts[2] = {g, u};
+        rc = ovh_weight_concat(parts, 2, L.st, &Y.gate_up);
+      }
     }
     ovh_weight_free(q);
     ovh_weight_free(k);
@@ -690,9 +697,28 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
     if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
     if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
-    if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
-    if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
-    if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+    if (L.silu_fused) {
+      // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
+      // (otherwise unused) gate/up buffers: codes [T][I], scales [T][I/32]
+      ovh::GemmArgs ga;
+      ga.M = (int)T;
+      ga.N = (int)(2 * I);
+      ga.Kb = (int)ovh::kb_of(H);
+      ga.Kp = 32 * ovh::kb_of(H);
+      ga.aq = aq;
+      ga.asc = asc;
+      ga.W = Y.gate_up->w.q;
+      ga.ws = Y.gate_up->w.scale;
+      ga.hq = reinterpret_cast<int8_t*>(gate);
+      ga.hsc = up;
+      ga.hKp = I;
+      OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
+      if ((rc = ovh_linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+    } else {
+      if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
+      if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
+      if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+    }
   }
   if ((rc = ovh_rmsnorm_quantize(T, H, x, L.final_norm, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
   if ((rc = ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st)) != OV_OK) return rc;
@@ -740,6 +766,7 @@ int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_te
   if (!L) return set_error(OV_ERR_INTERNAL, "out of host memory");
   L->cfg = *cfg;
   L->st = static_cast<hipStream_t>(stream);
+  L->silu_fused = cfg->inter % 64 == 0;
   int rc = OV_OK;
   if (hipMalloc(reinterpret_cast<void**>(&L->d_overflow), sizeof(uint32_t)) != hipSuccess ||
       hipMemset(L->d_overflow, 0, sizeof(uint32_t)) != hipSuccess)

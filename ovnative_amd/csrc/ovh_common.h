@@ -63,4 +63,26 @@ __device__ __forceinline__ float quant_block_lane(const float v[4], int nvalid, 
   return __fdiv_rn(amax, 127.0f);
 }
 
+// silu(g) * u as the reference's exp256 lanes compute it (ops_cpu.cpp:75-92,
+// 144-198 as its GCC build compiles them: the range reduction x - n*ln2 and
+// the final "1 + p*2^n" are fused).
+__device__ __forceinline__ float silu_up_lane(float g, float u) {
+  float x = __fsub_rn(0.0f, g);
+  x = fminf(x, 88.0f);   // minps(x, 88) yields 88 for NaN, as fminf does
+  x = fmaxf(x, -87.0f);
+  const float n = rintf(__fmul_rn(x, 1.4426950408889634f));
+  const float r = fmaf(-n, 0.6931471805599453f, x);
+  float p = 1.0f / 720;
+  p = fmaf(p, r, 1.0f / 120);
+  p = fmaf(p, r, 1.0f / 24);
+  p = fmaf(p, r, 1.0f / 6);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  const float sc = __int_as_float((ni + 127) << 23);
+  const float d = fmaf(p, sc, 1.0f);
+  return __fmul_rn(__fdiv_rn(g, d), u);
+}
+
 }  // namespace ovh

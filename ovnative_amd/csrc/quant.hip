@@ -166,24 +166,6 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
 // through a double-precision exp rounded once to float (glibc's expf is within
 // 0.502 ulp, so the two can differ for inputs whose exp lies within ~0.002 ulp
 // of a rounding midpoint).
-__device__ __forceinline__ float silu_up_lane(float g, float u) {
-  float x = __fsub_rn(0.0f, g);
-  x = fminf(x, 88.0f);   // minps(x, 88) yields 88 for NaN, as fminf does
-  x = fmaxf(x, -87.0f);
-  const float n = rintf(__fmul_rn(x, 1.4426950408889634f));
-  const float r = fmaf(-n, 0.6931471805599453f, x);
-  float p = 1.0f / 720;
-  p = fmaf(p, r, 1.0f / 120);
-  p = fmaf(p, r, 1.0f / 24);
-  p = fmaf(p, r, 1.0f / 6);
-  p = fmaf(p, r, 0.5f);
-  p = fmaf(p, r, 1.0f);
-  p = fmaf(p, r, 1.0f);
-  const int ni = (int)n;
-  const float sc = __int_as_float((ni + 127) << 23);
-  const float d = fmaf(p, sc, 1.0f);
-  return __fmul_rn(__fdiv_rn(g, d), u);
-}
 
 __device__ __forceinline__ float silu_up_tail(float g, float u) {
   const float e = (float)exp(-(double)g);

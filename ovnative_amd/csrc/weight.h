@@ -1,0 +1,19 @@
+// The device weight behind the ABI's opaque OvhWeight handle, and the
+// library-internal weight transforms the runner uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "gemm.h"
+
+struct OvhWeight {
+  ovh::DeviceWeight w;
+};
+
+namespace ovh {
+// gate [I, K] and up [I, K] (I % 64 == 0) -> one weight of 2I rows in which
+// 32-row block tile c holds gate rows 16c..16c+15 then up rows 16c..16c+15
+// (scales alike): the operand of the SiLU-fused GEMM mode.
+int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
+                        OvhWeight** out);
+}  // namespace ovh
