@@ -156,6 +156,65 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
   }
 }
 
+// Rows of 256*P columns (P <= 4; the LM's hidden sizes), one wavefront per row:
+// lane l owns k = 256p + 4l..+3, which is also the 4-value slot of quantisation
+// block 8p + l/8, so the row never has to be re-read.  For the sum of squares
+// the row is staged in LDS transposed, chain j (elements j, j+8, ...) as one
+// contiguous run, and lanes 0..7 stream their chains with ds_read_b128.  Same
+// arithmetic, in the same order, as rmsnorm_quantize_kernel.
+template <int P>
+__global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ w,
+                                                                   float eps,
+                                                                   int8_t* __restrict__ aq,
+                                                                   float* __restrict__ asc) {
+  constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
+  __shared__ __attribute__((aligned(16))) float xt[8 * TP];
+  const int lane = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const float* row = x + r * cols;
+  f32x4 xv[P], wv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) xv[p] = *reinterpret_cast<const f32x4*>(row + 256 * p + 4 * lane);
+#pragma unroll
+  for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
+  // element 256p + 4l + c -> chain 4(l&1) + c, position 32p + l/2
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xt[(4 * (lane & 1) + c) * TP + 32 * p + (lane >> 1)] = xv[p][c];
+  __syncthreads();
+  float part = 0.f;
+  if (lane < 8) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < T; t += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&xt[lane * TP + t]);
+      acc = fmaf(v[0], v[0], acc);
+      acc = fmaf(v[1], v[1], acc);
+      acc = fmaf(v[2], v[2], acc);
+      acc = fmaf(v[3], v[3], acc);
+    }
+    part = acc;
+  }
+  float sum = __shfl(part, 0);
+#pragma unroll
+  for (int j = 1; j < 8; ++j) sum = __fadd_rn(sum, __shfl(part, j));
+  const float scale =
+      __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
+  int8_t* qrow = aq + r * cols;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(xv[p][i], scale), wv[p][i]);
+    uint32_t codes;
+    const float s = quant_block_lane(v, 4, &codes);
+    *reinterpret_cast<uint32_t*>(qrow + 256 * p + 4 * lane) = codes;
+    if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // silu_mul_quantize_f32: cpp/src/backend/cpu/ops_cpu.cpp:144-198.
 //
@@ -236,6 +295,19 @@ size_t rmsnorm_quantize_smem(int64_t cols) {
 hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
                                    float eps, int8_t* aq, float* asc, hipStream_t st) {
   const int64_t Kb = kb_of(cols);
+  if (cols % 256 == 0 && cols <= 1024 && aligned16(x) && aligned16(w)) {
+    const dim3 grid((unsigned)rows), block(64);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, block, 0, st, x, w, eps, aq, asc);
+    };
+    switch (cols / 256) {
+      case 1: go(rmsnorm_quantize_rows_kernel<1>); break;
+      case 2: go(rmsnorm_quantize_rows_kernel<2>); break;
+      case 3: go(rmsnorm_quantize_rows_kernel<3>); break;
+      default: go(rmsnorm_quantize_rows_kernel<4>); break;
+    }
+    return hipGetLastError();
+  }
   const int rpb = rms_rows_per_block(rows);
   const size_t smem = sizeof(float) * (size_t)rpb * (size_t)(cols + 8);
   const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(64 * rpb);

@@ -240,7 +240,8 @@ def test_large_m_properties(oracle):
 # ---------------------------------------------------------------------------
 # fused producers at LM shapes vs the oracle
 
-@pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (13, 100)])
+@pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (40, 256), (7, 512),
+                                 (9, 768), (13, 100), (5, 1280)])
 def test_rmsnorm_quantize_vs_oracle(oracle, M, K):
     import ovnative_amd as ov
     rng = np.random.default_rng(M + K)
