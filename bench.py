@@ -19,9 +19,11 @@ inputs are synthetic token ids.
 value    = int8 linear throughput of the whole step: 2*M*N*K summed over every
            linear of the forward, divided by the measured step time (attention,
            norms, embedding and sampling included in that time), TOPS;
-roofline = the dominant kernel (merged gate/up GEMM, M=600 N=6144 K=1024),
-           timed with HIP events on the stream it runs on, against the dense
-           int8 MFMA peak;
+roofline = the kernel with the largest share of the step: the residual GEMM
+           (o_proj, K=2048, and down, K=3072; M=600, N=1024, accumulating into
+           the fp32 hidden state), 28 launches of each on distinct weights timed
+           with HIP events on the stream they run on, against the dense int8
+           MFMA peak;
 cpu_baseline = the reference's own LM::forward (cpp/src/model/lm.cpp, compiled
            from source into oracle/_ref) on the same checkpoint and batch, on
            the host's cores, when its AVX-VNNI int8-nk dispatch is available;
@@ -57,10 +59,11 @@ def attention_flops(cfg: dict, seq: int, batch: int, layers: int) -> int:
     return layers * batch * cfg["n_heads"] * 4 * seq * seq * cfg["head_dim"]
 
 
-def gate_up_traffic():
-    """HBM bytes per launch of the merged gate/up GEMM, from the committed PMC
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
-    path = os.path.join(ROOT, "profiles", "gemm_gate_up_m600_traffic.json")
+def residual_traffic():
+    """HBM bytes per launch of the residual GEMM (mean of the o_proj and down
+    launches), from the committed PMC summary (FETCH_SIZE + WRITE_SIZE, scaled
+    by the copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", "gemm_residual_m600_traffic.json")
     try:
         with open(path) as f:
             return json.load(f)["hbm_bytes_per_launch"]
@@ -77,6 +80,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--workload", choices=("step", "m16384"), default="step",
+                   help="step: BASELINE config 4 (the metric); m16384: config 5, one forward "
+                        "of 8 requests x CFG 2 x seq 1024 (M = 16384)")
     return p.parse_args()
 
 
@@ -130,19 +136,19 @@ def make_checkpoint(cfg: dict, seed: int = 0):
     return ts
 
 
-def make_inputs(cfg: dict, seed: int = 1):
-    """The CFG batch of tts.cpp:175-213: row 0 = cond prompt (TEXT text + audio),
+def make_inputs(cfg: dict, seed: int = 1, seq: int = SEQ, text: int = TEXT):
+    """The CFG batch of tts.cpp:175-213: row 0 = cond prompt (text + audio),
     row 1 = uncond (the target slice, then mask tokens attending to themselves)."""
     import numpy as np
     rng = np.random.default_rng(seed)
-    Cb, V, S = cfg["n_codebooks"], cfg["audio_vocab"], SEQ
-    T = S - TEXT
+    Cb, V, S, TEXT_ = cfg["n_codebooks"], cfg["audio_vocab"], seq, text
+    T = S - TEXT_
     ids = np.full((2, Cb, S), V - 1, np.int64)
-    ids[0, :, TEXT:] = rng.integers(0, V - 1, (Cb, T))
-    ids[0, 0, :TEXT] = rng.integers(0, cfg["vocab"], TEXT)
-    ids[1, :, :T] = ids[0, :, TEXT:]
+    ids[0, :, TEXT_:] = rng.integers(0, V - 1, (Cb, T))
+    ids[0, 0, :TEXT_] = rng.integers(0, cfg["vocab"], TEXT_)
+    ids[1, :, :T] = ids[0, :, TEXT_:]
     am = np.zeros((2, S), np.uint8)
-    am[0, TEXT:] = 1
+    am[0, TEXT_:] = 1
     am[1, :T] = 1
     attn = np.ones((2, S, S), np.uint8)
     attn[1] = 0
@@ -150,6 +156,13 @@ def make_inputs(cfg: dict, seed: int = 1):
     attn[1, np.arange(T, S), np.arange(T, S)] = 1
     pos = np.tile(np.arange(S, dtype=np.int64), (2, 1))
     return ids, am, attn, pos, T
+
+
+def make_requests(cfg: dict, requests: int, seq: int, text: int = TEXT):
+    """`requests` independent CFG pairs stacked into one batch of 2*requests rows."""
+    import numpy as np
+    parts = [make_inputs(cfg, seed=10 + r, seq=seq, text=text)[:4] for r in range(requests)]
+    return tuple(np.concatenate([p[i] for p in parts]) for i in range(4))
 
 
 # ---------------------------------------------------------------------------
@@ -172,44 +185,56 @@ class LmStep:
         return self.lm.sample(base, SEQ, base + self.plane, SEQ, self.T, 2.0, 5.0)
 
 
-def time_gate_up(cfg: dict, layers: int, reps: int = 4) -> float:
-    """Average duration (ms) of the dominant kernel, the merged gate/up GEMM at
-    M = 600: reps x layers back-to-back launches over distinct weights (as in
-    the step), between one pair of HIP events on the stream they run on."""
+def time_residual(cfg: dict, layers: int, M: int, reps: int = 4):
+    """The residual GEMM as the step runs it: `layers` o_proj (K = heads*128) and
+    `layers` down (K = inter) launches on distinct weights, accumulating into one
+    fp32 [M, hidden] buffer, reps times back to back between one pair of HIP
+    events on the stream they run on.  Returns (ms per launch, int8 ops per
+    launch on average)."""
     import torch
     import ovnative_amd as ov
-    H, I, M = cfg["hidden"], cfg["inter"], SEQ * CFG_BATCH
+    H, QD, I = cfg["hidden"], cfg["n_heads"] * cfg["head_dim"], cfg["inter"]
     g = torch.Generator(device="cuda").manual_seed(7)
-    ws = []
-    for _ in range(layers):
-        q = torch.randint(-127, 128, (2 * I, H), generator=g, device="cuda", dtype=torch.int8)
-        s = torch.rand(2 * I, generator=g, device="cuda") * 1e-3 + 1e-4
-        ws.append(ov.Weight.from_device(q, s))
-    x = torch.randn((M, H), generator=g, device="cuda")
-    aq, asc = ov.rmsnorm_quantize(x, torch.ones(H, device="cuda"), 1e-6)
-    gate = torch.empty((M, I), device="cuda")
-    up = torch.empty((M, I), device="cuda")
-    for w in ws[:2]:
-        ov.linear_q_sliced(aq, asc, w, [I, I], outs=[gate, up])
+
+    def weight(n, k):
+        q = torch.randint(-127, 128, (n, k), generator=g, device="cuda", dtype=torch.int8)
+        s = torch.rand(n, generator=g, device="cuda") * 1e-3 + 1e-4
+        return ov.Weight.from_device(q, s)
+
+    wo = [weight(H, QD) for _ in range(layers)]
+    wd = [weight(H, I) for _ in range(layers)]
+    ao = ov.s8_nk_quantize(torch.randn((M, QD), generator=g, device="cuda"))
+    ad = ov.s8_nk_quantize(torch.randn((M, I), generator=g, device="cuda"))
+    x = torch.zeros((M, H), device="cuda")
+
+    def once():
+        for a, b in zip(wo, wd):
+            ov.linear_q(ao[0], ao[1], a, x, accumulate=True)
+            ov.linear_q(ad[0], ad[1], b, x, accumulate=True)
+
+    once()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        for w in ws:
-            ov.linear_q_sliced(aq, asc, w, [I, I], outs=[gate, up])
+        once()
     e1.record()
     torch.cuda.synchronize()
-    for w in ws:
+    for w in wo + wd:
         w.free()
-    return e0.elapsed_time(e1) / (reps * layers)
+    n = reps * 2 * layers
+    return e0.elapsed_time(e1) / n, (2 * M * H * QD + 2 * M * H * I) / 2
 
 
 # ---------------------------------------------------------------------------
 # CPU baseline (reported beside the GPU, not optimised)
 
-def cpu_baseline(cfg: dict, tensors, budget_s: float):
+def cpu_baseline(cfg: dict, tensors, budget_s: float, batch=None):
+    """batch = (ids, am, attn, pos) (default: the config-4 CFG batch)."""
     import oracle
-    ids, am, attn, pos, T = make_inputs(cfg)
-    M = SEQ * CFG_BATCH
+    ids, am, attn, pos = batch if batch is not None else make_inputs(cfg)[:4]
+    B, S = am.shape
+    M = B * S
     threads = oracle.Oracle().num_threads()
     ref = None
     if oracle.reference_available():
@@ -242,7 +267,7 @@ def cpu_baseline(cfg: dict, tensors, budget_s: float):
             "cores": threads,
             "kind": "reference",
             "sample": (f"reference LM::forward (lm.cpp, {ref.kernel_name()} int8-nk kernels) on the "
-                       f"same checkpoint: {cfg['n_layers']} layers, B=2, S={SEQ}, median of "
+                       f"same checkpoint: {cfg['n_layers']} layers, B={B}, S={S}, median of "
                        f"{len(times)} forwards (host sampling pass not included)"),
             "ms_per_step": round(sec * 1e3, 2),
         }
@@ -253,7 +278,7 @@ def cpu_baseline(cfg: dict, tensors, budget_s: float):
         return None
     nl = 2
     table = {t.name: (t.array, t.scales, t.layout == 1) for t in tensors}
-    segs = [(attn[b], SEQ, b * SEQ) for b in range(2)]
+    segs = [(attn[b], S, b * S) for b in range(B)]
     sub = dict(cfg, n_layers=nl)
     o.lm_forward(sub, table, ids, am, segs, pos.reshape(-1))
     times = []
@@ -269,9 +294,80 @@ def cpu_baseline(cfg: dict, tensors, budget_s: float):
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle restatement, {nl}-layer prefix at B=2 S={SEQ}, median of {len(times)}",
+        "sample": f"oracle restatement, {nl}-layer prefix at B={B} S={S}, median of {len(times)}",
         "ms_per_step": None,
     }
+
+
+def run_m16384(args, cfg: dict, tensors) -> None:
+    """8 concurrent requests x CFG 2 x seq 1024 (M = 16384)
+    through the 28-layer LM; one step = one forward (logits left on the device)."""
+    import torch
+    import ovnative_amd as ov
+    requests, seq = 8, 1024
+    batch = make_requests(cfg, requests, seq)
+    ids, am, attn, pos = batch
+    B = 2 * requests
+    M = B * seq
+    lm = ov.LM.from_tensors(tensors, ov.LmConfig(**cfg))
+    lm.set_device_sampling(True)
+    for _ in range(args.warmup):
+        lm.forward(ids, am, attn, pos, host_logits=False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        lm.forward(ids, am, attn, pos, host_logits=False)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    lm.close()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    ops = linear_ops(cfg, M, args.layers)
+    tops = ops / (ms_step * 1e-3) / 1e12
+    log(f"M={M} forward {ms_step:.2f} ms ({tops:.1f} linear TOPS)")
+    rs_ms, rs_ops = time_residual(cfg, args.layers, M, reps=1)
+    rs_tops = rs_ops / (rs_ms * 1e-3) / 1e12
+    cpu = None if args.no_cpu else cpu_baseline(cfg, tensors, args.cpu_seconds, batch)
+    line = {
+        "metric": "int8 linear TOPS & % roofline; LM ms/step (seq 300, CFG batch 2)",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"BASELINE config 5: one forward of the {args.layers}-layer LM over "
+                         f"{requests} requests x CFG 2 x seq {seq} (M={M}; each request the "
+                         "tts.cpp cond/uncond pair), logits left on the device"),
+            "model": "Qwen3-0.6B-shaped LM (hidden 1024, 16/8 heads x 128, inter 3072, 28 layers)",
+            "global_batch": B,
+            "seq_len": seq,
+            "parallelism": "single GPU",
+            "step_linear_gop": round(ops / 1e9, 2),
+            "step_attention_gflop": round(attention_flops(cfg, seq, B, args.layers) / 1e9, 2),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": f"gemm16 residual (o_proj K=2048 and down K=3072; M={M}, N=1024, += x)",
+            "achieved": round(rs_tops, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(rs_tops / PEAK_INT8_TOPS, 4),
+            "traffic": None,
+            "avg_ms": round(rs_ms, 5),
+        },
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
 
 
 def main():
@@ -291,6 +387,9 @@ def main():
     M = SEQ * CFG_BATCH
     t_setup = time.perf_counter()
     tensors = make_checkpoint(cfg)
+    if args.workload == "m16384":
+        run_m16384(args, cfg, tensors)
+        return
     step = LmStep(cfg, tensors)
     log(f"checkpoint + upload {time.perf_counter() - t_setup:.1f}s")
     for _ in range(args.warmup):
@@ -326,9 +425,8 @@ def main():
     gen_ms = (time.perf_counter() - t_gen) * 1e3
     log(f"32-step decode {gen_ms:.1f} ms")
 
-    gu_ms = time_gate_up(cfg, args.layers)
-    gu_ops = 2 * M * (2 * cfg["inter"]) * cfg["hidden"]
-    gu_tops = gu_ops / (gu_ms * 1e-3) / 1e12
+    rs_ms, rs_ops = time_residual(cfg, args.layers, M)
+    rs_tops = rs_ops / (rs_ms * 1e-3) / 1e12
     step.lm.close()
 
     cpu = None if args.no_cpu else cpu_baseline(cfg, tensors, args.cpu_seconds)
@@ -362,13 +460,13 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm16 gate/up merged (M=600, N=6144, K=1024)",
-            "achieved": round(gu_tops, 2),
+            "kernel": "gemm16 residual (o_proj K=2048 and down K=3072; M=600, N=1024, += x)",
+            "achieved": round(rs_tops, 2),
             "peak": PEAK_INT8_TOPS,
             "unit": "TFLOP/s",
-            "frac": round(gu_tops / PEAK_INT8_TOPS, 4),
-            "traffic": gate_up_traffic(),
-            "avg_ms": round(gu_ms, 5),
+            "frac": round(rs_tops / PEAK_INT8_TOPS, 4),
+            "traffic": residual_traffic(),
+            "avg_ms": round(rs_ms, 5),
         },
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),

@@ -10,6 +10,11 @@ from ovnative_amd import ovw1
 
 SMALL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, inter=512,
              vocab=300, audio_vocab=33, n_codebooks=8, rms_eps=1e-6, rope_theta=1e6)
+# One decoder layer at the LM's real widths with the real
+# 8 x 1025 audio head; the text table is cut to 2048 rows (it only has to hold
+# the mask id the unconditional row carries in its text slots).
+FULL1 = dict(n_layers=1, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, inter=3072,
+             vocab=2048, audio_vocab=1025, n_codebooks=8, rms_eps=1e-6, rope_theta=1e6)
 
 
 def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True):

@@ -21,7 +21,7 @@ Bars:
 import numpy as np
 import pytest
 
-from lm_fixture import SMALL, make_inputs, make_lm
+from lm_fixture import FULL1, SMALL, make_inputs, make_lm
 
 pytestmark = pytest.mark.gpu
 
@@ -99,6 +99,27 @@ def test_forward_bit_exact_given_attention(oracle, small_lm, split):
     segs = [(attn[b], S, b * S) for b in range(B)]
     hybrid = oracle.lm_forward(SMALL, table, ids, am, segs, pos.reshape(-1),
                                attention=_device_attention(SMALL, split))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
+def test_full_width_layer_bit_exact_given_attention(oracle):
+    """one Qwen3-0.6B-shaped decoder layer (hidden 1024, 16/8
+    heads x 128, inter 3072; plus the embeddings and the 8 x 1025 head) on the
+    tts.cpp CFG batch at M = 2 x 300: the runner's logits equal, bit for bit, the
+    oracle's forward with the device attention substituted."""
+    import ovnative_amd as ov
+    ts, table = make_lm(3, FULL1)
+    ids, am, attn, pos = make_inputs(5, FULL1, 2, 300, 40)
+    lm = ov.LM.from_tensors(ts, _cfg(FULL1))
+    try:
+        got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
+    finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(FULL1, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(FULL1))
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
