@@ -774,6 +774,269 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     *reinterpret_cast<f32x4*>(dst + j) = f32x4{ov[j], ov[j + 1], ov[j + 2], ov[j + 3]};
 }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// ---------------------------------------------------------------------------
+// Long-sequence form of the split-f16 attention.  In the form above every
+// workgroup (32 query rows) streams its KV head's whole planes through its
+// wavefronts' registers; at seq 1024 that is ~1 MB per workgroup per head and
+// the L2 -> CU traffic, not the matrix core, sets the time.  Here a workgroup
+// covers 128 query-head rows: its 4 wavefronts are the G heads of one KV group
+// times 128/G queries (wave w: head kvh*G + w%G, rows 32*(w/G)..+31 of the
+// tile), each 32-key block of K and V is moved into LDS once (DMA, double
+// buffered) and read by all four, and every wavefront walks all keys itself, so
+// there is no merge.  Per element the arithmetic is the form above's (three f16
+// products, base-2 online softmax, same masks, same quantised epilogue).
+// LDS planes of a block, 16-byte chunks XOR-swizzled so the fragment reads are
+// conflict-free: K [32 keys][16 chunks of 8 d], chunk slot = c ^ (key & 15);
+// V [128 rows][4 chunks of 8 keys] (the rows and key order of the global V
+// planes), chunk slot = c ^ ((row >> 2) & 3).
+constexpr int kLdsPlane = 32 * kAttnD;  // halves per plane per block
+// Longest segment from which this form is used: measured with 2 segments of S
+// rows, 16/8 heads (short form vs this, us): S = 512: 39.8 vs 45.6, 768: 81.8
+// vs 66.3, 1024: 138.6 vs 90.8.
+constexpr int kLdsMinRows = 640;
+
+template <bool kBits>
+__global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs args, AttnSplit sp,
+                                                                     int qtiles, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) _Float16 kv[2][4][kLdsPlane];  // kh, kl, vh, vl
+  __shared__ float xs[kAttnWaves][kAttnQ];                               // per-wave row exchange
+  __shared__ float ms[kAttnWaves][kAttnQ];
+  const int G = args.group;  // 4 % G == 0 (host)
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r32 = lane & 31, hf = lane >> 5;
+  const int n_kv = args.n_heads / G;
+  const int task = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (task >= args.n_segs * n_kv * qtiles) return;
+  const int qt = task % qtiles;
+  const int sk = task / qtiles;  // segment * n_kv + kv head
+  const int sidx = sk / n_kv;
+  const int kvh = sk - sidx * n_kv;
+  const AttnSeg seg = args.segs[sidx];
+  const int S = seg.rows;
+  const int QT = kAttnWaves * kAttnQ / G;  // queries per workgroup
+  if (qt * QT >= S) return;               // uniform for the workgroup
+  const int h = kvh * G + wave % G;
+  const int q0 = qt * QT + kAttnQ * (wave / G);
+  const bool live = q0 < S;  // uniform for the wavefront; dead ones still move data
+
+  // ---- Q fragments in registers: chunk c = d 16c + 8hf .. +7 of row q0 + r32
+  h8 qh[8], ql[8];
+  {
+    const int qr = min(q0 + r32, S - 1);
+    const float* src = args.q + seg.q_off + (int64_t)qr * args.q_stride + (int64_t)h * kAttnD + 8 * hf;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src + 16 * c);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 16 * c + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        _Float16 a, b;
+        split16(x0[j], a, b);
+        qh[c][j] = a;
+        ql[c][j] = b;
+        split16(x1[j], a, b);
+        qh[c][4 + j] = a;
+        ql[c][4 + j] = b;
+      }
+    }
+  }
+
+  // ---- DMA sources.  Wave w moves plane w of each block (8 x 1 KiB):
+  // K planes (w < 2): slot s = 64 i + lane -> key s/16, chunk (s%16) ^ (key&15);
+  // V planes: slot s -> row s/4, chunk (s%4) ^ ((row>>2)&3).
+  const int64_t krow0 = seg.kv_off / args.kv_stride;
+  const _Float16* plane = wave == 0 ? sp.kh : wave == 1 ? sp.kl : wave == 2 ? sp.vh : sp.vl;
+  auto issue = [&](int blk) __attribute__((always_inline)) {
+    const int t0 = blk * kAttnK;
+    _Float16* dst = &kv[blk & 1][wave][0];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = 64 * i + lane;
+      const _Float16* src;
+      if (wave < 2) {
+        const int key = s >> 4, c = (s & 15) ^ (key & 15);
+        const int kr = min(t0 + key, S - 1);
+        src = plane + (krow0 + kr) * args.kv_stride + (int64_t)kvh * kAttnD + 8 * c;
+      } else {
+        const int row = s >> 2, c = (s & 3) ^ ((row >> 2) & 3);
+        src = plane + ((int64_t)kvh * kAttnD + row) * sp.vt_cols + sp.vt_off[sidx] + t0 + 8 * c;
+      }
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (lds_void_t*)(dst + 512 * i), 16, 0, 0);
+    }
+  };
+
+  const int qrow = min(q0 + r32, S - 1);
+  const uint32_t* mrow = kBits && seg.bits ? seg.bits + (int64_t)qrow * ((S + 31) >> 5) : nullptr;
+  const float* brow = !kBits && seg.bias ? seg.bias + (int64_t)qrow * S : nullptr;
+  const float sl2 = args.scale * kLog2e;
+  constexpr float kMaskedBias = -1e30f * kLog2e;
+
+  f32x16 o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[c][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int kslot = r32 * kAttnD;  // this lane's key row in a K plane
+
+  const int nblk = (S + kAttnK - 1) / kAttnK;
+  issue(0);
+  for (int blk = 0; blk < nblk; ++blk) {
+    wait_vm_lgkm<0>();              // this wavefront's DMA for block blk (and Q) landed
+    __builtin_amdgcn_s_barrier();   // ... and the others'; block blk-1's slot is free
+    if (blk + 1 < nblk) issue(blk + 1);
+    if (!live) continue;
+    const int t0 = blk * kAttnK;
+    const _Float16* kb = &kv[blk & 1][0][0];
+    // ---- S^T = K Q^T
+    f32x16 st;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st[e] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int off = kslot + 8 * ((2 * c + hf) ^ (r32 & 15));
+      const h8 khf = *reinterpret_cast<const h8*>(kb + off);
+      const h8 klf = *reinterpret_cast<const h8*>(kb + kLdsPlane + off);
+      st = mfma_h(klf, qh[c], st);
+      st = mfma_h(khf, ql[c], st);
+      st = mfma_h(khf, qh[c], st);
+    }
+    // ---- bias of this lane's 16 keys (key of element e: t0 + 8(e/4) + 4hf + e%4)
+    float bv[16];
+    if (kBits) {
+      const uint32_t mword = (mrow ? mrow[blk] : 0xffffffffu) >> (4 * hf);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+    } else if (brow) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bv[e] = __fmul_rn(brow[min(t0 + 8 * (e >> 2) + 4 * hf + (e & 3), S - 1)], kLog2e);
+    }
+    float p[16];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int t = t0 + 8 * (e >> 2) + 4 * hf + (e & 3);
+      float y = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
+      y = t < S ? y : -INFINITY;
+      p[e] = y;
+      bmax = fmaxf(bmax, y);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float m_new = fmaxf(m_run, bmax);
+    const float m_ref = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      p[e] = __builtin_amdgcn_exp2f(p[e] - m_ref);
+      psum = __fadd_rn(psum, p[e]);
+    }
+    psum = __fadd_rn(psum, __shfl_xor(psum, 32));
+    l_run = fmaf(l_run, alpha, psum);
+    m_run = m_new;
+
+    if (hf == 0) xs[wave][r32] = alpha;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&xs[wave][8 * g + 4 * hf]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- O += P V
+    const _Float16* vb = kb + 2 * kLdsPlane;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      h8 ph, pl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 a, b;
+        split16(p[8 * c + j], a, b);
+        ph[j] = a;
+        pl[j] = b;
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int row = 32 * db + r32;
+        const int off = row * kAttnK + 8 * ((2 * c + hf) ^ ((row >> 2) & 3));
+        const h8 vhf = *reinterpret_cast<const h8*>(vb + off);
+        const h8 vlf = *reinterpret_cast<const h8*>(vb + kLdsPlane + off);
+        o[db] = mfma_h(pl, vhf, o[db]);
+        o[db] = mfma_h(ph, vlf, o[db]);
+        o[db] = mfma_h(ph, vhf, o[db]);
+      }
+    }
+  }
+  if (!live) return;
+
+  // ---- epilogue: row i of o[c][e] is query q0 + 8(e/4) + 4hf + e%4, column
+  // d = 4*r32 + c; its l and m live in lane i (exchanged through LDS)
+  if (hf == 0) {
+    xs[wave][r32] = l_run;
+    ms[wave][r32] = m_run;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 l4 = *reinterpret_cast<const f32x4*>(&xs[wave][8 * g + 4 * hf]);
+    const f32x4 m4 = *reinterpret_cast<const f32x4*>(&ms[wave][8 * g + 4 * hf]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 8 * g + 4 * hf + e;
+      const bool valid = q0 + i < S;
+      f32x4 v;
+      if (m4[e] < kMaskedLog2) {  // fully masked row
+        v = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        const float inv = __fdiv_rn(1.f, l4[e]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __fmul_rn(o[c][4 * g + e], inv);
+      }
+      if (sp.aq) {
+        // 32-column block = lanes r32 = 8b..8b+7 of this half: amax by xor 1, 2, 4
+        float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        a = fmaxf(a, __shfl_xor(a, 1));
+        a = fmaxf(a, __shfl_xor(a, 2));
+        a = fmaxf(a, __shfl_xor(a, 4));
+        const float qinv = a > 0.f ? __fdiv_rn(127.0f, a) : 0.f;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          packed |= (uint32_t)(uint8_t)(int8_t)quant_q(v[c], qinv) << (8 * c);
+        if (valid) {
+          const int64_t row = seg.q_off / args.q_stride + q0 + i;
+          const int64_t col = (int64_t)h * kAttnD + 4 * r32;
+          *reinterpret_cast<uint32_t*>(sp.aq + row * args.out_stride + col) = packed;
+          if ((r32 & 7) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(a, 127.0f);
+        }
+      } else if (valid) {
+        float* dst = args.out + seg.q_off + (int64_t)(q0 + i) * args.out_stride +
+                     (int64_t)h * kAttnD + 4 * r32;
+        *reinterpret_cast<f32x4*>(dst) = v;
+      }
+    }
+  }
+}
+
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                   hipStream_t st) {
   if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
@@ -810,6 +1073,21 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   if ((uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
       (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
     return hipErrorInvalidValue;
+  if (max_rows >= kLdsMinRows && kAttnWaves % args.group == 0) {
+    // long segments: K/V blocks shared through LDS by 128 query-head rows
+    const int QT = kAttnWaves * kAttnQ / args.group;
+    const int qtiles = (max_rows + QT - 1) / QT;
+    const int tasks = args.n_segs * (args.n_heads / args.group) * qtiles;
+    const int per_xcd = (tasks + 7) / 8;
+    const dim3 grid((unsigned)(8 * per_xcd));
+    if (mask_bits)
+      hipLaunchKernelGGL(attention_split_lds_kernel<true>, grid, dim3(256), 0, st, args, sp, qtiles,
+                         per_xcd);
+    else
+      hipLaunchKernelGGL(attention_split_lds_kernel<false>, grid, dim3(256), 0, st, args, sp,
+                         qtiles, per_xcd);
+    return hipGetLastError();
+  }
   // 1-D grid of 8 * per_xcd workgroups (XCD-aware task order in the kernel)
   const int qtiles = (max_rows + kAttnQ - 1) / kAttnQ;
   const int tasks = args.n_segs * args.n_heads * qtiles;

@@ -82,13 +82,15 @@ def _device_attention(cfg, split=True):
     return run
 
 
-@pytest.mark.parametrize("split", [True, False], ids=["split_f16", "fp32"])
-def test_forward_bit_exact_given_attention(oracle, small_lm, split):
+@pytest.mark.parametrize("split,seq", [(True, 70), (False, 70), (True, 660)],
+                         ids=["split_f16", "fp32", "split_f16_long"])
+def test_forward_bit_exact_given_attention(oracle, small_lm, split, seq):
     """Every step except attention is the reference's arithmetic bit for bit:
     with the device attention kernel substituted into the oracle's forward, the
-    runner's logits are identical (both attention forms of the runner)."""
+    runner's logits are identical (both attention forms of the runner; seq 660
+    takes the long-segment split kernel)."""
     ts, table, lm = small_lm
-    ids, am, attn, pos = make_inputs(11, SMALL, 2, 70, 12)
+    ids, am, attn, pos = make_inputs(11, SMALL, 2, seq, 12)
     lm.set_attention(split)
     try:
         got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
