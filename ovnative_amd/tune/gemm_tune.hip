@@ -29,6 +29,10 @@ extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const 
     case 13: return launch_cfg16<64, 64, 2, 2, 4, 3>(a, mode, s);
     case 14: return launch_cfg16<32, 32, 2, 2, 8, 2>(a, mode, s);
     case 15: return launch_cfg16<64, 32, 2, 2, 4, 3>(a, mode, s);
+    case 16: return launch_cfg16<32, 32, 2, 2, 4, 3>(a, mode, s);
+    case 17: return launch_cfg16<32, 32, 2, 2, 4, 4>(a, mode, s);
+    case 18: return launch_cfg16<32, 32, 2, 2, 8, 3>(a, mode, s);
+    case 19: return launch_cfg16<32, 64, 2, 2, 4, 3>(a, mode, s);
   }
   return -1;
 }

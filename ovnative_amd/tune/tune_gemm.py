@@ -16,7 +16,8 @@ class DW(C.Structure):
 # (LDS DMA ring): s<BN>x<BM>w<waves>[b<blocks per stage>][n<ring stages>]
 cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x128', 6: '64x32', 7: '32x32',
         8: 's32x32w4', 9: 's64x32w4', 10: 's128x64w8', 11: 's128x64w8n3', 12: 's64x32w8',
-        13: 's64x64w4n3', 14: 's32x32w4b8', 15: 's64x32w4xn3'}
+        13: 's64x64w4n3', 14: 's32x32w4b8', 15: 's64x32w4xn3', 16: 's32x32w4n3', 17: 's32x32w4n4',
+        18: 's32x32w4b8n3', 19: 's32x64w4n3'}
 if len(sys.argv) > 1:
     cfgs = {k: v for k, v in cfgs.items() if str(k) in sys.argv[1].split(',')}
 shapes = [(600, 6144, 1024), (600, 4096, 1024), (600, 1024, 2048), (600, 1024, 3072), (600, 8192, 1024),
