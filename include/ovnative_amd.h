@@ -259,6 +259,10 @@ void ovh_lm_set_device_sampling(OvhLm* lm, int on);
  * products.  No reference counterpart (the CUDA runner picks its attention
  * kernel from the sequence length and environment variables, cuda_lm.cu:1106-1115). */
 void ovh_lm_set_attention(OvhLm* lm, int split_f16);
+/* Forward launches: 1 = captured once per layout into a HIP graph and replayed
+ * (default), 0 = launched one by one.  Both give the same bits.  No reference
+ * counterpart (the CUDA runner launches its kernels one by one). */
+void ovh_lm_set_graphs(OvhLm* lm, int on);
 /* LmRunnerSampleThunk (cuda_lm.h:39-41): the per-step guidance + argmax pass
  * (tts.cpp:296-326) on device logit planes; pred/scores host [C, target_len]. */
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

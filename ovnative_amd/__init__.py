@@ -70,6 +70,7 @@ SIGNATURES = {
     "ovh_attention_split": (_int, [_p, _int, _int, _int, _int, _p, _i64, _p, _p, _i64, _f32, _p,
                                    _i64, _p]),
     "ovh_lm_set_attention": (None, [_p, _int]),
+    "ovh_lm_set_graphs": (None, [_p, _int]),
 }
 
 
@@ -500,6 +501,10 @@ class LM:
 
     def set_attention(self, split_f16: bool) -> None:
         load().ovh_lm_set_attention(self.handle, int(bool(split_f16)))
+
+    def set_graphs(self, on: bool) -> None:
+        """Replay the forward as a captured HIP graph (default) or launch its kernels one by one."""
+        load().ovh_lm_set_graphs(self.handle, int(bool(on)))
 
     def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
                target_len: int, guidance: float, layer_penalty: float):

@@ -321,8 +321,10 @@ __device__ __forceinline__ void wait_vm_lgkm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.
-template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE>
+// NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.  PIPE:
+// the stage loop runs as a software pipeline (below); without it each stage
+// is read, multiplied and folded block by block.
+template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE>
 __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
@@ -338,7 +340,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   constexpr bool EVEN = TILES % NW == 0;
   __shared__ __attribute__((aligned(16))) int8_t smem[NST][STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave index in a scalar register: the DMA slots and the wait below branch on it
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
   const int n_tiles = (a.N + BN - 1) / BN;
   int ntile, mtile;
@@ -391,10 +394,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
                                          (lds_void_t*)(base + SCL + c * BM * 16), 16, 0, 0);
     }
   };
-  // Waiting for stage s: the DMA ops issued after it (stages s+1 .. s+NST-2)
-  // may stay in flight.  TPW per stage is the fewest any wavefront issues, so
-  // the count is conservative for the wavefront that also moves the scales.
-  constexpr int LATER = (EVEN ? TPW : TPW - 1) * (NST - 2);
+  // Waiting for stage s: the DMA ops this wavefront issued after it (stages
+  // s+1 .. s+NST-2) may stay in flight.  Per stage, wavefronts below
+  // TILES % NW issue TPW ops, the others TPW - 1 (all TPW when EVEN), and the
+  // last one SB/4 more for the scales; each waits on its own count, since a
+  // smaller one would also wait for part of the next stage.
+  constexpr int OPS_HI = TPW, OPS_LO = EVEN ? TPW : TPW - 1;
+  constexpr int LATER_HI = OPS_HI * (NST - 2), LATER_LO = OPS_LO * (NST - 2);
+  constexpr int LATER_LAST = (OPS_LO + SB / 4) * (NST - 2);
+  const bool last_wave = wave == NW - 1, hi_wave = EVEN || wave < TILES % NW;
   // fragment byte offsets inside a block tile (see above)
   const int q = lane >> 4;
   const int frag = ((q >> 1) * 32 + (lane & 15)) * 16 + (q & 1) * 8;
@@ -416,46 +424,123 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 #pragma unroll
     for (int j = 0; j < FM; ++j) f[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int s = 0; s < NST - 1; ++s)
-    if (s < nstages) issue(s);
-  for (int s = 0; s < nstages; ++s) {
-    if (s + NST - 2 < nstages)
-      wait_vm_lgkm<LATER>();  // this wavefront's DMA for stage s landed
-    else
+  // Software pipeline over ring stages: while the exact epilogue of stage s
+  // runs on the VALU, the fragments of stage s + 1 come in from LDS and its
+  // block products go to the matrix core.  Fragments, scales and block
+  // products of a stage are held in registers between those steps; the
+  // epilogue still folds the blocks into f in block order.
+  int64_t af[SB][FN], bf[SB][FM];
+  f32x4 sc[SB / 4][FM], sc_next[SB / 4][FM];
+  i32x4 acc[SB][FN][FM];
+  // Stage s in LDS for every wavefront: this wavefront's DMA for it landed
+  // (and its own LDS reads, so its slot reads are done), then the others'.
+  // A bare s_barrier: __syncthreads()'s release fence would also drain the
+  // later stages' DMA (vmcnt(0)).
+  auto wait_stage = [&](int s) __attribute__((always_inline)) {
+    if (s + NST - 2 < nstages) {
+      if (last_wave)
+        wait_vm_lgkm<LATER_LAST>();
+      else if (hi_wave)
+        wait_vm_lgkm<LATER_HI>();
+      else
+        wait_vm_lgkm<LATER_LO>();
+    } else {
       wait_vm_lgkm<0>();
-    // ... and every other wavefront's.  A bare s_barrier: __syncthreads()'s
-    // release fence would also drain the later stages' DMA (vmcnt(0)).
+    }
     __builtin_amdgcn_s_barrier();
-    // slot (s + NST - 1) % NST was read in iteration s - 1, which every
-    // wavefront has left
-    if (s + NST - 1 < nstages) issue(s + NST - 1);
+  };
+  auto read_stage = [&](int s, f32x4 (&scs)[SB / 4][FM]) __attribute__((always_inline)) {
     const int8_t* base = smem[s % NST];
-    f32x4 sc[SB / 4][FM];
 #pragma unroll
     for (int c = 0; c < SB / 4; ++c)
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        sc[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
-                                                   (wm * TM + 16 * j + (lane & 15)) * 16);
+        scs[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
+                                                    (wm * TM + 16 * j + (lane & 15)) * 16);
 #pragma unroll
     for (int bb = 0; bb < SB; ++bb) {
-      int64_t af[FN], bf[FM];
 #pragma unroll
       for (int i = 0; i < FN; ++i)
-        af[i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
+        af[bb][i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        bf[j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+        bf[bb][j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+    }
+  };
+  auto products = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int bb = 0; bb < SB; ++bb)
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j) {
-          const i32x4 acc = mfma16_i8(af[i], bf[j]);
+        for (int j = 0; j < FM; ++j) acc[bb][i][j] = mfma16_i8(af[bb][i], bf[bb][j]);
+  };
+  auto epilogue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int bb = 0; bb < SB; ++bb)
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            f[i][j][e] = fmaf((float)acc[e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
-        }
+            f[i][j][e] = fmaf((float)acc[bb][i][j][e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+  };
+
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < nstages) issue(s);
+  if constexpr (PIPE) {
+    wait_stage(0);
+    if (NST - 1 < nstages) issue(NST - 1);
+    read_stage(0, sc);
+    products();
+    for (int s = 0; s + 1 < nstages; ++s) {
+      wait_stage(s + 1);
+      // slot (s + NST) % NST held stage s, whose reads every wavefront has
+      // finished before the barrier
+      if (s + NST < nstages) issue(s + NST);
+      read_stage(s + 1, sc_next);
+      epilogue();
+      products();
+#pragma unroll
+      for (int c = 0; c < SB / 4; ++c)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) sc[c][j] = sc_next[c][j];
+    }
+    epilogue();
+  } else {
+    for (int s = 0; s < nstages; ++s) {
+      wait_stage(s);
+      // slot (s + NST - 1) % NST was read in iteration s - 1, which every
+      // wavefront has left
+      if (s + NST - 1 < nstages) issue(s + NST - 1);
+      const int8_t* base = smem[s % NST];
+#pragma unroll
+      for (int c = 0; c < SB / 4; ++c)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          sc[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
+                                                     (wm * TM + 16 * j + (lane & 15)) * 16);
+#pragma unroll
+      for (int bb = 0; bb < SB; ++bb) {
+        int64_t a1[FN], b1[FM];
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          a1[i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          b1[j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const i32x4 p = mfma16_i8(a1[i], b1[j]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              f[i][j][e] = fmaf((float)p[e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+          }
+      }
     }
   }
 
@@ -548,26 +633,28 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 }
 
 // Launchable when Kb % SB == 0.
-template <int BN, int BM, int WN, int WM, int SB, int NST>
+template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
 hipError_t launch_cfg16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   if (a.Kb % SB) return hipErrorInvalidValue;
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
   const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
   if (mode == kAccumulate)
-    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumulate>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumulate, PIPE>), grid, block, 0,
+                       st, a);
   else
-    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kStore>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kStore, PIPE>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
 // The SiLU-fused mode (wave tiles 64 rows wide: BN / WN == 64).
-template <int BN, int BM, int WN, int WM, int SB, int NST>
+template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
 hipError_t launch_cfg16_silu(const GemmArgs& a, hipStream_t st) {
   static_assert(BN / WN == 64, "four 16-row tiles per wavefront");
   if (a.Kb % SB || a.N % 128 || !a.hq || !a.hsc || a.hKp < a.N / 2) return hipErrorInvalidValue;
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
   const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
-  hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kSiluQuant>), grid, block, 0, st, a);
+  hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kSiluQuant, PIPE>), grid, block, 0, st,
+                     a);
   return hipGetLastError();
 }
 
@@ -606,22 +693,28 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // MFMAs), mid-size ones 64x64, and skinny M or N = 1024 one-wave 32x32 tiles,
   // which give the most wavefronts for the few output tiles there are.
   const int64_t M = a.M, N = a.N;
+  // Stage loop: the software pipeline pays where a wavefront holds few output
+  // tiles (32x32 and 64x32 workgroups, the SiLU tile at M = 600: 17.7 vs
+  // 19.4 us); with 2x2 tiles per wavefront its extra live registers cost more
+  // than it hides (128x64 at M = 16384, N = 6144: 325 us block by block, 464
+  // pipelined).
   if (mode == kSiluQuant) {
     if (a.Kb % 4) return hipErrorInvalidValue;
-    return launch_cfg16_silu<128, 64, 2, 2, 4, 2>(a, st);
+    if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);
+    return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, st);
   }
   if (mode != kDumpBlocks && a.Kb % 4 == 0) {
     // 16x16 wave tiles (sweep on MI355X, LM shapes at M = 128 / 600 / 16384):
     // many small workgroups for the skinny and N = 1024 shapes, 128x64 tiles
-    // of 8 wavefronts for wide N at M >= 512.
-    if (M >= 2048) return launch_cfg16<128, 64, 4, 2, 4, 3>(a, mode, st);
-    if (M >= 512 && N >= 6144) return launch_cfg16<128, 64, 4, 2, 4, 2>(a, mode, st);
-    if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2>(a, mode, st);
-    // skinny M streams cold weights: a 4-stage ring keeps 3 stages of DMA in
-    // flight (M = 128, weights from HBM: 284 vs 232 GB/s over a layer's seven
-    // projections)
-    if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 4>(a, mode, st);
-    return launch_cfg16<32, 32, 2, 2, 4, 2>(a, mode, st);
+    // of 8 wavefronts for wide N at M >= 512 and for every N at M >= 2048.
+    if (M >= 2048 || (M >= 512 && N >= 6144))
+      return launch_cfg16<128, 64, 4, 2, 4, 2, false>(a, mode, st);
+    if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, st);
+    // skinny M streams cold weights: a 3-stage ring keeps 2 stages of DMA in
+    // flight (M = 128, weights from HBM, a layer's seven projections: 318 GB/s;
+    // 2 stages 225, 4 stages 284)
+    if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
+    return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, st);
   }
   if (M >= 2048 || (M >= 512 && N >= 6144)) return launch_cfg<128, 64, 2, 2>(a, mode, st);
   if (M >= 256) return launch_cfg<64, 64, 2, 2>(a, mode, st);

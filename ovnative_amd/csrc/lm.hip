@@ -267,6 +267,13 @@ struct OvhLm {
   bool silu_fused = false;
   // attention: split-f16 products (default) or fp32; overflow flag of the split
   bool attn_split = true;
+  // The forward's launches as one HIP graph, captured per layout (graph_key)
+  // and replayed; own_st is the runner's stream when the caller gave none
+  // (graphs are not captured on the legacy default stream).
+  bool use_graphs = true;
+  hipGraphExec_t graph = nullptr;
+  std::vector<int64_t> graph_key;
+  hipStream_t own_st = nullptr;
   uint32_t* d_overflow = nullptr;
   // RoPE tables of the last position list (rebuilt only when it changes)
   std::vector<int64_t> tab_pos;
@@ -291,6 +298,8 @@ struct OvhLm {
     if (h_out) (void)hipHostFree(h_out);
     if (d_tab) (void)hipFree(d_tab);
     if (d_overflow) (void)hipFree(d_overflow);
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (own_st) (void)hipStreamDestroy(own_st);
   }
 };
 
@@ -618,35 +627,22 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     if (bias_off[i] >= 0)
       std::memcpy(L.h_in + in_mask + bias_off[i], segs[i].mask,
                   (size_t)segs[i].rows * (size_t)segs[i].rows);
-  OVH_HIP(hipMemcpyAsync(d_in, L.h_in, in_bytes, hipMemcpyHostToDevice, st), "upload inputs");
-  OVH_HIP(hipEventRecord(L.in_done, st), "hipEventRecord");
+  // each segment's mask: bias rows (fp32 attention) or bit words (split form)
   std::vector<OvhAttnSegment> asegs(segs.size());
   std::vector<const uint32_t*> seg_bits(segs.size(), nullptr);
   for (size_t i = 0; i < segs.size(); ++i) {
     const float* bias = nullptr;
     if (bias_off[i] >= 0) {
-      const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
-      uint8_t* m = d_mask + bias_off[i];
-      if (split) {
-        uint32_t* bw = static_cast<uint32_t*>(at(b_bits)) + bits_off[i];
-        OVH_HIP(ovh::launch_mask_bits(m, segs[i].rows, bw, st), "mask_bits launch");
-        seg_bits[i] = bw;
-      } else {
-        float* bb = static_cast<float*>(at(b_bias)) + bias_off[i];
-        hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
-                           0, st, m, bb, n);
-        OVH_HIP(hipGetLastError(), "mask_to_bias launch");
-        bias = bb;
-      }
+      if (split)
+        seg_bits[i] = static_cast<uint32_t*>(at(b_bits)) + bits_off[i];
+      else
+        bias = static_cast<float*>(at(b_bias)) + bias_off[i];
     }
     asegs[i] = OvhAttnSegment{bias, segs[i].rows, segs[i].row0 * QD, segs[i].row0 * KVD};
   }
   float *cosb = nullptr, *sinb = nullptr;
   int rc = rope_tables_cached(L, pos, T, &cosb, &sinb);
   if (rc != OV_OK) return rc;
-  hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)T), dim3(256), 0, st, d_ids, d_am, seq,
-                     (int)C, H, L.tok, L.aud, L.d_offsets, x);
-  OVH_HIP(hipGetLastError(), "embed launch");
 
   const float scale = 1.f / std::sqrt((float)D);
   ovh::AttnArgs aargs{};
@@ -673,55 +669,119 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     sp.aq = aq;  // attention writes the o_proj input already quantised
     sp.asc = asc;
   }
-  const int64_t qkv_n[3] = {QD, KVD, KVD};
-  float* qkv_c[3] = {q, k, v};
-  const int64_t gu_n[2] = {I, I};
-  float* gu_c[2] = {gate, up};
-  for (const OvhLm::Layer& Y : L.layers) {
-    if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln1, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
-    if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st)) != OV_OK) return rc;
-    if (split) {
-      // q/k norm + RoPE, f16 planes of k and V, then attention
-      OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
-                                             sinb, c.rms_eps, aargs, sp, max_rows, st),
-              "qk_norm_rope launch");
-      OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
-    } else {
-      if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb,
-                                 sinb, c.rms_eps, st)) != OV_OK)
-        return rc;
-      if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
-                              QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
-        return rc;
+  // The inputs go up first, in one copy; the staging buffer may be refilled
+  // once it is done.
+  OVH_HIP(hipMemcpyAsync(d_in, L.h_in, in_bytes, hipMemcpyHostToDevice, st), "upload inputs");
+  OVH_HIP(hipEventRecord(L.in_done, st), "hipEventRecord");
+  // Everything else the forward does on the device, in stream order: masks,
+  // embedding, the layers, final norm and head.
+  auto enqueue = [&]() -> int {
+    int rc = OV_OK;
+    for (size_t i = 0; i < segs.size(); ++i) {
+      if (bias_off[i] < 0) continue;
+      const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
+      const uint8_t* m = d_mask + bias_off[i];
+      if (split) {
+        OVH_HIP(ovh::launch_mask_bits(m, segs[i].rows, const_cast<uint32_t*>(seg_bits[i]), st),
+                "mask_bits launch");
+      } else {
+        hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                           0, st, m, const_cast<float*>(asegs[i].bias), n);
+        OVH_HIP(hipGetLastError(), "mask_to_bias launch");
+      }
     }
-    if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
-    if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
-    if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
-    if (L.silu_fused) {
-      // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
-      // (otherwise unused) gate/up buffers: codes [T][I], scales [T][I/32]
-      ovh::GemmArgs ga;
-      ga.M = (int)T;
-      ga.N = (int)(2 * I);
-      ga.Kb = (int)ovh::kb_of(H);
-      ga.Kp = 32 * ovh::kb_of(H);
-      ga.aq = aq;
-      ga.asc = asc;
-      ga.W = Y.gate_up->w.q;
-      ga.ws = Y.gate_up->w.scale;
-      ga.hq = reinterpret_cast<int8_t*>(gate);
-      ga.hsc = up;
-      ga.hKp = I;
-      OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
-      if ((rc = ovh_linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st)) != OV_OK) return rc;
-    } else {
-      if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
-      if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
-      if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+    hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)T), dim3(256), 0, st, d_ids, d_am, seq,
+                       (int)C, H, L.tok, L.aud, L.d_offsets, x);
+    OVH_HIP(hipGetLastError(), "embed launch");
+    const int64_t qkv_n[3] = {QD, KVD, KVD};
+    float* qkv_c[3] = {q, k, v};
+    const int64_t gu_n[2] = {I, I};
+    float* gu_c[2] = {gate, up};
+    for (const OvhLm::Layer& Y : L.layers) {
+      if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln1, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+      if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st)) != OV_OK) return rc;
+      if (split) {
+        // q/k norm + RoPE, f16 planes of k and V, then attention
+        OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
+                                               sinb, c.rms_eps, aargs, sp, max_rows, st),
+                "qk_norm_rope launch");
+        OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
+      } else {
+        if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb,
+                                   sinb, c.rms_eps, st)) != OV_OK)
+          return rc;
+        if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
+                                QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
+          return rc;
+      }
+      if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
+      if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
+      if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+      if (L.silu_fused) {
+        // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
+        // (otherwise unused) gate/up buffers: codes [T][I], scales [T][I/32]
+        ovh::GemmArgs ga;
+        ga.M = (int)T;
+        ga.N = (int)(2 * I);
+        ga.Kb = (int)ovh::kb_of(H);
+        ga.Kp = 32 * ovh::kb_of(H);
+        ga.aq = aq;
+        ga.asc = asc;
+        ga.W = Y.gate_up->w.q;
+        ga.ws = Y.gate_up->w.scale;
+        ga.hq = reinterpret_cast<int8_t*>(gate);
+        ga.hsc = up;
+        ga.hKp = I;
+        OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
+        if ((rc = ovh_linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+      } else {
+        if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
+        if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
+        if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+      }
     }
+    if ((rc = ovh_rmsnorm_quantize(T, H, x, L.final_norm, c.rms_eps, aq, asc, st)) != OV_OK)
+      return rc;
+    return ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st);
+  };
+
+  if (!L.use_graphs) {
+    if ((rc = enqueue()) != OV_OK) return rc;
+  } else {
+    // One graph per forward layout: the shapes, the segments and their masks,
+    // and every buffer address the launches take.  A changed layout (other
+    // lengths, a grown arena, new RoPE tables) is captured anew; the same
+    // layout replays over the new inputs the upload above brought.
+    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, (int64_t)segs.size(),
+                                (int64_t)in_bytes, (int64_t)(intptr_t)L.arena,
+                                (int64_t)(intptr_t)cosb, (int64_t)(intptr_t)sinb};
+    for (size_t i = 0; i < segs.size(); ++i) {
+      key.push_back(segs[i].rows);
+      key.push_back(segs[i].row0);
+      key.push_back(bias_off[i]);
+      key.push_back(bits_off[i]);
+    }
+    if (!L.graph || key != L.graph_key) {
+      if (L.graph) OVH_HIP(hipGraphExecDestroy(L.graph), "hipGraphExecDestroy");
+      L.graph = nullptr;
+      L.graph_key.clear();
+      OVH_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+      const int erc = enqueue();
+      hipGraph_t g = nullptr;
+      const hipError_t e = hipStreamEndCapture(st, &g);
+      if (erc != OV_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return erc;
+      }
+      OVH_HIP(e, "end capture");
+      const hipError_t ei = hipGraphInstantiate(&L.graph, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (ei != hipSuccess) L.graph = nullptr;
+      OVH_HIP(ei, "hipGraphInstantiate");
+      L.graph_key = key;
+    }
+    OVH_HIP(hipGraphLaunch(L.graph, st), "hipGraphLaunch");
   }
-  if ((rc = ovh_rmsnorm_quantize(T, H, x, L.final_norm, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
-  if ((rc = ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st)) != OV_OK) return rc;
   L.logits = logits;
   return OV_OK;
 }
@@ -766,6 +826,16 @@ int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_te
   if (!L) return set_error(OV_ERR_INTERNAL, "out of host memory");
   L->cfg = *cfg;
   L->st = static_cast<hipStream_t>(stream);
+  if (!L->st) {
+    // A stream of the runner's own, created with the default flags: it stays
+    // ordered with the legacy default stream the caller uses, and the forward
+    // can be captured into a graph on it.
+    if (hipStreamCreate(&L->own_st) != hipSuccess) {
+      delete L;
+      return set_error(OV_ERR_INTERNAL, "hipStreamCreate");
+    }
+    L->st = L->own_st;
+  }
   L->silu_fused = cfg->inter % 64 == 0;
   int rc = OV_OK;
   if (hipMalloc(reinterpret_cast<void**>(&L->d_overflow), sizeof(uint32_t)) != hipSuccess ||
@@ -846,6 +916,10 @@ void ovh_lm_set_device_sampling(OvhLm* lm, int on) {
 
 void ovh_lm_set_attention(OvhLm* lm, int split_f16) {
   if (lm) lm->attn_split = split_f16 != 0;
+}
+
+void ovh_lm_set_graphs(OvhLm* lm, int on) {
+  if (lm) lm->use_graphs = on != 0;
 }
 
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

@@ -21,18 +21,41 @@ extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const 
   }
   if (Kb % 4) return -1;  // 16x16 variants: 4- or 8-block stages only
   switch (cfg) {
-    case 8: return launch_cfg16<32, 32, 2, 2, 4, 2>(a, mode, s);
-    case 9: return launch_cfg16<64, 32, 4, 1, 4, 2>(a, mode, s);
-    case 10: return launch_cfg16<128, 64, 4, 2, 4, 2>(a, mode, s);
-    case 11: return launch_cfg16<128, 64, 4, 2, 4, 3>(a, mode, s);
-    case 12: return launch_cfg16<64, 32, 4, 2, 4, 2>(a, mode, s);
-    case 13: return launch_cfg16<64, 64, 2, 2, 4, 3>(a, mode, s);
-    case 14: return launch_cfg16<32, 32, 2, 2, 8, 2>(a, mode, s);
-    case 15: return launch_cfg16<64, 32, 2, 2, 4, 3>(a, mode, s);
-    case 16: return launch_cfg16<32, 32, 2, 2, 4, 3>(a, mode, s);
-    case 17: return launch_cfg16<32, 32, 2, 2, 4, 4>(a, mode, s);
-    case 18: return launch_cfg16<32, 32, 2, 2, 8, 3>(a, mode, s);
-    case 19: return launch_cfg16<32, 64, 2, 2, 4, 3>(a, mode, s);
+    case 8: return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, s);
+    case 9: return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, s);
+    case 10: return launch_cfg16<128, 64, 4, 2, 4, 2, true>(a, mode, s);
+    case 11: return launch_cfg16<128, 64, 4, 2, 4, 3, true>(a, mode, s);
+    case 12: return launch_cfg16<64, 32, 4, 2, 4, 2, true>(a, mode, s);
+    case 13: return launch_cfg16<64, 64, 2, 2, 4, 3, true>(a, mode, s);
+    case 14: return launch_cfg16<32, 32, 2, 2, 8, 2, true>(a, mode, s);
+    case 15: return launch_cfg16<64, 32, 2, 2, 4, 3, true>(a, mode, s);
+    case 16: return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, s);
+    case 17: return launch_cfg16<32, 32, 2, 2, 4, 4, true>(a, mode, s);
+    case 18: return launch_cfg16<32, 32, 2, 2, 8, 3, true>(a, mode, s);
+    case 19: return launch_cfg16<32, 64, 2, 2, 4, 3, true>(a, mode, s);
+    case 20: return launch_cfg16<32, 32, 2, 2, 4, 6, true>(a, mode, s);
+    case 21: return launch_cfg16<64, 32, 4, 1, 4, 4, true>(a, mode, s);
+    case 22: return launch_cfg16<128, 64, 4, 2, 4, 4, true>(a, mode, s);
+    case 23: return launch_cfg16<64, 32, 4, 1, 4, 3, true>(a, mode, s);
+    case 24: return launch_cfg16<64, 64, 2, 2, 4, 4, true>(a, mode, s);
+    // the same tiles with the block-by-block stage loop
+    case 30: return launch_cfg16<32, 32, 2, 2, 4, 2, false>(a, mode, s);
+    case 31: return launch_cfg16<64, 32, 4, 1, 4, 2, false>(a, mode, s);
+    case 32: return launch_cfg16<128, 64, 4, 2, 4, 2, false>(a, mode, s);
+    case 33: return launch_cfg16<128, 64, 4, 2, 4, 3, false>(a, mode, s);
+    case 34: return launch_cfg16<32, 32, 2, 2, 4, 4, false>(a, mode, s);
+    case 35: return launch_cfg16<64, 32, 2, 2, 4, 3, false>(a, mode, s);
   }
   return -1;
+}
+
+// The SiLU-fused gate/up tile (interleaved weights) in either stage-loop form.
+extern "C" int tune_gemm_silu(int pipe, int M, int N, int Kb, const int8_t* aq, const float* asc,
+                              const int8_t* W, const float* ws, int8_t* hq, float* hsc,
+                              int64_t hKp, void* st) {
+  GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
+  a.W = W; a.ws = ws; a.hq = hq; a.hsc = hsc; a.hKp = hKp;
+  hipStream_t s = (hipStream_t)st;
+  return pipe ? launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, s)
+              : launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, s);
 }

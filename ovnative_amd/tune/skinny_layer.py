@@ -42,7 +42,10 @@ def run(j, w):
     name, n, k = shapes[j]
     aq, asc = acts[k]
     if lib is None:
-        ov.linear_q(aq, asc, w, outs[n])
+        # the C ABI entry itself: a Python wrapper per launch would leave the
+        # GPU waiting on the host at these kernel times
+        ov.load().ovh_linear_q(M, aq.data_ptr(), asc.data_ptr(), w.handle, outs[n].data_ptr(), n,
+                               0, st)
     else:
         dw = DW.from_address(w.handle.value)
         lib.tune_gemm(cfg, M, n, k // 32, aq.data_ptr(), asc.data_ptr(), dw.q, dw.scale,

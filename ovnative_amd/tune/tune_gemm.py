@@ -12,12 +12,16 @@ lib = C.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libgemm_t
 lib.tune_gemm.argtypes = [C.c_int]*4 + [C.c_void_p]*5 + [C.c_int, C.c_void_p]
 class DW(C.Structure):
     _fields_ = [('N', C.c_int64), ('K', C.c_int64), ('Npad', C.c_int64), ('Kb', C.c_int64), ('Kp', C.c_int64), ('q', C.c_void_p), ('scale', C.c_void_p)]
-# 0-7: the 32x32-tile kernel (register-staged); 8-15: the 16x16-tile kernel
-# (LDS DMA ring): s<BN>x<BM>w<waves>[b<blocks per stage>][n<ring stages>]
+# 0-7: the 32x32-tile kernel (register-staged); 8-24: the 16x16-tile kernel
+# (LDS DMA ring, software-pipelined stage loop): s<BN>x<BM>w<waves>[b<blocks per
+# stage>][n<ring stages>]; 30-35: 16x16 tiles with the block-by-block stage loop (b...)
 cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x128', 6: '64x32', 7: '32x32',
         8: 's32x32w4', 9: 's64x32w4', 10: 's128x64w8', 11: 's128x64w8n3', 12: 's64x32w8',
         13: 's64x64w4n3', 14: 's32x32w4b8', 15: 's64x32w4xn3', 16: 's32x32w4n3', 17: 's32x32w4n4',
-        18: 's32x32w4b8n3', 19: 's32x64w4n3'}
+        18: 's32x32w4b8n3', 19: 's32x64w4n3', 20: 's32x32w4n6', 21: 's64x32w4n4', 22: 's128x64w8n4',
+        23: 's64x32w4n3', 24: 's64x64w4n4',
+        30: 'b32x32w4', 31: 'b64x32w4', 32: 'b128x64w8', 33: 'b128x64w8n3', 34: 'b32x32w4n4',
+        35: 'b64x32w4xn3'}
 if len(sys.argv) > 1:
     cfgs = {k: v for k, v in cfgs.items() if str(k) in sys.argv[1].split(',')}
 shapes = [(600, 6144, 1024), (600, 4096, 1024), (600, 1024, 2048), (600, 1024, 3072), (600, 8192, 1024),

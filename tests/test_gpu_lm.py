@@ -263,3 +263,54 @@ def test_generate_matches_restated_loop(small_lm):
                                seed=77)
     assert np.all(got != V - 1)                       # every position decoded
     assert np.array_equal(got, want)
+
+
+def test_graph_replays_match_eager(small_lm):
+    """The forward captured as a HIP graph and replayed gives the eager launches'
+    bits on every replay: two id sets of one layout alternate over six replays,
+    with eager runner work, a forward of another layout and torch work on the
+    device between them; the CFG decode loop gives the same tokens either way."""
+    import ovnative_amd as ov
+    ts, table, lm = small_lm
+    sets = [make_inputs(s, SMALL, 2, 64, 10) for s in (31, 32)]
+    other = make_inputs(33, SMALL, 2, 40, 6)
+    lm.set_graphs(False)
+    try:
+        want = [lm.forward(*x) for x in sets]
+        want_other = lm.forward(*other)
+    finally:
+        lm.set_graphs(True)
+    assert not np.array_equal(want[0], want[1])
+    scratch = torch.randn(1 << 20, device="cuda")
+    for rep in range(6):
+        x = sets[rep % 2]
+        got = lm.forward(*x)
+        assert np.array_equal(got.view(np.int32), want[rep % 2].view(np.int32)), rep
+        # eager work between the replays
+        scratch.mul_(1.0001).add_(0.5)
+        torch.cuda.synchronize()
+        if rep == 2:
+            lm.set_graphs(False)
+            try:
+                assert np.array_equal(lm.forward(*other).view(np.int32), want_other.view(np.int32))
+            finally:
+                lm.set_graphs(True)
+        if rep == 3:   # another layout captured and replayed in between
+            assert np.array_equal(lm.forward(*other).view(np.int32), want_other.view(np.int32))
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    S, T = 40, 14
+    rng = np.random.default_rng(5)
+    prompt = np.full((Cb, S), V - 1, np.int64)
+    prompt[0, :S - T - 6] = rng.integers(0, SMALL["vocab"], S - T - 6)
+    prompt[:, S - T - 6:S - T] = rng.integers(0, V - 1, (Cb, 6))
+    am = np.zeros(S, np.uint8)
+    am[S - T - 6:] = 1
+    opts = ov.GenOptions(num_steps=6, guidance_scale=2.0, t_shift=0.1, layer_penalty=5.0,
+                         position_temperature=5.0, seed=3)
+    got = lm.generate(prompt, am, T, opts)
+    lm.set_graphs(False)
+    try:
+        eager = lm.generate(prompt, am, T, opts)
+    finally:
+        lm.set_graphs(True)
+    assert np.array_equal(got, eager)
