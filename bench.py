@@ -207,10 +207,19 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4):
     ad = ov.s8_nk_quantize(torch.randn((M, I), generator=g, device="cuda"))
     x = torch.zeros((M, H), device="cuda")
 
+    # straight through the C ABI: at ~10 us per launch a Python wrapper per call
+    # would leave the GPU waiting on the host
+    lib = ov.load()
+    st = torch.cuda.current_stream().cuda_stream
+    calls = []
+    for a, b in zip(wo, wd):
+        calls.append((M, ao[0].data_ptr(), ao[1].data_ptr(), a.handle, x.data_ptr(), H, 1, st))
+        calls.append((M, ad[0].data_ptr(), ad[1].data_ptr(), b.handle, x.data_ptr(), H, 1, st))
+
     def once():
-        for a, b in zip(wo, wd):
-            ov.linear_q(ao[0], ao[1], a, x, accumulate=True)
-            ov.linear_q(ad[0], ad[1], b, x, accumulate=True)
+        for c in calls:
+            if lib.ovh_linear_q(*c) != 0:
+                raise RuntimeError("ovh_linear_q failed")
 
     once()
     torch.cuda.synchronize()
