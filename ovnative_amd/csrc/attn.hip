@@ -1,6 +1,7 @@
 // Attention side of one decoder layer for gfx950: RoPE tables, fused per-head
 // RMSNorm + RoPE, and bidirectional GQA attention with an additive bias.
 #include <cstdint>
+#include <type_traits>
 
 #include "attn.h"
 #include "ovh_common.h"
@@ -475,6 +476,9 @@ constexpr int kQPad = kAttnD + 8;  // LDS row of a Q plane, in halves
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kMaskedLog2 = -1e29f * kLog2e;
 
+// The mask word of a segment without a mask: every key visible.
+__device__ const uint32_t kAllVisible[1] = {0xffffffffu};
+
 template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, AttnSplit sp,
                                                                  int qtiles, int per_xcd) {
@@ -500,7 +504,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   const int S = seg.rows;
   const int q0 = qt * kAttnQ;
   if (q0 >= S) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index in a scalar register: the key loop's trip count and block
+  // starts are then uniform and its loads unconditional
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
 
   // ---- Q rows q0..q0+31 of head h -> hi/lo planes in LDS (16 values per thread)
@@ -527,8 +533,8 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     }
   }
 
-  // Wave-uniform plane bases and 32-bit per-lane element offsets (the launcher
-  // checks that every offset fits).
+  // Wave-uniform plane bases and 32-bit per-lane byte offsets (the launcher
+  // checks that every offset fits), so the loads take a scalar base.
   const int64_t krow0 = seg.kv_off / args.kv_stride;  // segment's first k row
   const _Float16* __restrict__ khb = sp.kh + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
   const _Float16* __restrict__ klb = sp.kl + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
@@ -540,21 +546,31 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   const uint32_t kstride = (uint32_t)args.kv_stride;
 
   // Mask of this lane's query row: bit words (kBits) or the additive bias row.
+  // Without mask words every block reads the one all-visible word, so the
+  // word's load is unconditional.
   const int qrow = min(q0 + r32, S - 1);
-  const uint32_t* mrow =
-      kBits && seg.bits ? seg.bits + (int64_t)qrow * ((S + 31) >> 5) : nullptr;
+  // (global address space spelled out: through the select the compiler would
+  // otherwise emit a flat load, which it can only wait for with vmcnt(0))
+  typedef const __attribute__((address_space(1))) uint32_t gword;
+  const bool has_bits = kBits && seg.bits;  // uniform
+  const gword* mrow = has_bits ? (const gword*)(seg.bits + (int64_t)qrow * ((S + 31) >> 5))
+                               : (const gword*)kAllVisible;
+  const int mstep = has_bits ? 1 : 0;
   const float* brow = !kBits && seg.bias ? seg.bias + (int64_t)qrow * S : nullptr;
   const bool bias_vec = brow && (S & 3) == 0 && (reinterpret_cast<uintptr_t>(seg.bias) & 15) == 0;
   const float sl2 = args.scale * kLog2e;
   constexpr float kMaskedBias = -1e30f * kLog2e;  // the mask's bias, in base-2 units
 
   h8 kh[8], kl[8], vh[8], vl[8];  // K: chunk c; V: 8 * (16-key chunk) + ... index 4c + db
+  auto ld = [](const _Float16* base, uint32_t elem) __attribute__((always_inline)) {
+    return *reinterpret_cast<const h8*>(reinterpret_cast<const char*>(base) + 2u * elem);
+  };
   auto load_k = [&](int t0) {
     const uint32_t off = (uint32_t)min(t0 + r32, S - 1) * kstride + 8 * hf;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      kh[c] = *reinterpret_cast<const h8*>(khb + (off + 16 * c));
-      kl[c] = *reinterpret_cast<const h8*>(klb + (off + 16 * c));
+      kh[c] = ld(khb, off + 16 * c);
+      kl[c] = ld(klb, off + 16 * c);
     }
   };
   auto load_v = [&](int t0) {
@@ -563,8 +579,8 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const uint32_t off = vlane + db * vstep + (uint32_t)(t0 + 16 * c);
-        vh[4 * c + db] = *reinterpret_cast<const h8*>(vhb + off);
-        vl[4 * c + db] = *reinterpret_cast<const h8*>(vlb + off);
+        vh[4 * c + db] = ld(vhb, off);
+        vl[4 * c + db] = ld(vlb, off);
       }
   };
 
@@ -577,23 +593,28 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
 
   // The mask form prefetches the next block's K and V; the float-bias form has
   // 16 more live values per lane and loads K and V at the start of each block.
+  // No load sits under a branch inside the key loop (where the paths join the
+  // compiler would wait for every load in flight): the wavefront's last block
+  // is peeled off as the one that prefetches nothing.
   constexpr bool kPrefetch = kBits;
   const int nblk = (S + kAttnK - 1) / kAttnK;
-  if (kPrefetch && wave < nblk) {
+  const int nb = wave < nblk ? (nblk - 1 - wave) / kAttnWaves + 1 : 0;  // this wavefront's blocks
+  if (kPrefetch && nb > 0) {
     load_k(wave * kAttnK);
     load_v(wave * kAttnK);
   }
   __syncthreads();  // Q planes written
 
-  for (int blk = wave; blk < nblk; blk += kAttnWaves) {
+  auto key_block = [&](int blk, auto next) __attribute__((always_inline)) {
+    constexpr bool kNext = kPrefetch && decltype(next)::value;
     const int t0 = blk * kAttnK;
-    const bool more = kPrefetch && blk + kAttnWaves < nblk;  // uniform for the wavefront
+    const int t_next = t0 + kAttnWaves * kAttnK;
     if (!kPrefetch) {
       load_k(t0);
       load_v(t0);
     }
     // this lane's 16 mask bits: bit 8g + i = key t0 + 8g + 4hf + i
-    const uint32_t mword = (mrow ? mrow[blk] : 0xffffffffu) >> (4 * hf);
+    const uint32_t mword = mrow[blk * mstep] >> (4 * hf);
     // ---- S^T = K Q^T (32 keys x 32 queries), three f16 products per chunk
     f32x16 st;
 #pragma unroll
@@ -609,15 +630,20 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     // the next block's fragments reuse these registers: keep the loads after
     // the products that read them
     __builtin_amdgcn_sched_barrier(0);
-    if (more) load_k(t0 + kAttnWaves * kAttnK);
+    if (kNext) load_k(t_next);
 
     // bias of this lane's 16 keys (key of element e: t0 + 8(e/4) + 4hf + e%4),
     // base-2 units
     float bv[16];
     if (kBits) {
+      if (has_bits) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+        for (int e = 0; e < 16; ++e)
+          bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bv[e] = 0.f;
+      }
     } else if (brow) {
       if (bias_vec) {
 #pragma unroll
@@ -640,13 +666,15 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     float p[16];
     float bmax = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int t = t0 + 8 * (e >> 2) + 4 * hf + (e & 3);
-      float y = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
-      y = t < S ? y : -INFINITY;
-      p[e] = y;
-      bmax = fmaxf(bmax, y);
+    for (int e = 0; e < 16; ++e)
+      p[e] = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
+    if (t0 + kAttnK > S) {  // keys past the segment (uniform: the last block only)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (t0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= S) p[e] = -INFINITY;
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bmax = fmaxf(bmax, p[e]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
     const float m_new = fmaxf(m_run, bmax);
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // all keys so far at -inf
@@ -694,8 +722,10 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (more) load_v(t0 + kAttnWaves * kAttnK);
-  }
+    if (kNext) load_v(t_next);
+  };
+  for (int i = 0; i + 1 < nb; ++i) key_block(wave + i * kAttnWaves, std::true_type{});
+  if (nb > 0) key_block(wave + (nb - 1) * kAttnWaves, std::false_type{});
 
   __syncthreads();  // every wavefront is done with the Q planes
   // merge the 4 key splits (output column of block db, lane r32: d = 4*r32 + db)
@@ -806,11 +836,17 @@ constexpr int kLdsMinRows = 640;
 template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs args, AttnSplit sp,
                                                                      int qtiles, int per_xcd) {
-  __shared__ __attribute__((aligned(16))) _Float16 kv[2][4][kLdsPlane];  // kh, kl, vh, vl
+  // Double buffer as two arrays (kh, kl, vh, vl planes each): with the block
+  // loop unrolled by parity, a block's reads and the next block's DMA touch
+  // different arrays, which the compiler can tell apart (one array would make
+  // it wait for the DMA before every read).
+  __shared__ __attribute__((aligned(16))) _Float16 kv0[4][kLdsPlane];
+  __shared__ __attribute__((aligned(16))) _Float16 kv1[4][kLdsPlane];
   __shared__ float xs[kAttnWaves][kAttnQ];                               // per-wave row exchange
   __shared__ float ms[kAttnWaves][kAttnQ];
   const int G = args.group;  // 4 % G == 0 (host)
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index in a scalar register: `live` and the block loop are uniform
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
   const int n_kv = args.n_heads / G;
   const int task = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
@@ -854,9 +890,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
   // V planes: slot s -> row s/4, chunk (s%4) ^ ((row>>2)&3).
   const int64_t krow0 = seg.kv_off / args.kv_stride;
   const _Float16* plane = wave == 0 ? sp.kh : wave == 1 ? sp.kl : wave == 2 ? sp.vh : sp.vl;
-  auto issue = [&](int blk) __attribute__((always_inline)) {
+  auto issue = [&](int blk, auto odd) __attribute__((always_inline)) {
     const int t0 = blk * kAttnK;
-    _Float16* dst = &kv[blk & 1][wave][0];
+    _Float16* dst = decltype(odd)::value ? &kv1[wave][0] : &kv0[wave][0];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int s = 64 * i + lane;
@@ -874,8 +910,14 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     }
   };
 
+  // mask words as in attention_split_kernel: the all-visible word when the
+  // segment has none, so the load is unconditional
+  typedef const __attribute__((address_space(1))) uint32_t gword;
   const int qrow = min(q0 + r32, S - 1);
-  const uint32_t* mrow = kBits && seg.bits ? seg.bits + (int64_t)qrow * ((S + 31) >> 5) : nullptr;
+  const bool has_bits = kBits && seg.bits;  // uniform
+  const gword* mrow = has_bits ? (const gword*)(seg.bits + (int64_t)qrow * ((S + 31) >> 5))
+                               : (const gword*)kAllVisible;
+  const int mstep = has_bits ? 1 : 0;
   const float* brow = !kBits && seg.bias ? seg.bias + (int64_t)qrow * S : nullptr;
   const float sl2 = args.scale * kLog2e;
   constexpr float kMaskedBias = -1e30f * kLog2e;
@@ -888,15 +930,22 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
   float m_run = -INFINITY, l_run = 0.f;
   const int kslot = r32 * kAttnD;  // this lane's key row in a K plane
 
+  // The last block is peeled off as the one that issues no DMA, so no load
+  // sits under a branch inside the loop.
   const int nblk = (S + kAttnK - 1) / kAttnK;
-  issue(0);
-  for (int blk = 0; blk < nblk; ++blk) {
+  issue(0, std::false_type{});
+  // block blk (odd: blk % 2 == 1, its planes in kv1), then the next block's DMA
+  auto key_block = [&](int blk, auto next, auto odd) __attribute__((always_inline)) {
+    constexpr bool kOdd = decltype(odd)::value;
+    // this lane's mask word, loaded ahead of the DMA issue so that waiting for
+    // it leaves the next block's DMA in flight
+    const uint32_t mword_raw = kBits ? (uint32_t)mrow[blk * mstep] : 0u;
     wait_vm_lgkm<0>();              // this wavefront's DMA for block blk (and Q) landed
     __builtin_amdgcn_s_barrier();   // ... and the others'; block blk-1's slot is free
-    if (blk + 1 < nblk) issue(blk + 1);
-    if (!live) continue;
+    if constexpr (decltype(next)::value) issue(blk + 1, std::integral_constant<bool, !kOdd>{});
+    if (!live) return;
     const int t0 = blk * kAttnK;
-    const _Float16* kb = &kv[blk & 1][0][0];
+    const _Float16* kb = kOdd ? &kv1[0][0] : &kv0[0][0];
     // ---- S^T = K Q^T
     f32x16 st;
 #pragma unroll
@@ -913,10 +962,15 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     // ---- bias of this lane's 16 keys (key of element e: t0 + 8(e/4) + 4hf + e%4)
     float bv[16];
     if (kBits) {
-      const uint32_t mword = (mrow ? mrow[blk] : 0xffffffffu) >> (4 * hf);
+      const uint32_t mword = mword_raw >> (4 * hf);
+      if (has_bits) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+        for (int e = 0; e < 16; ++e)
+          bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bv[e] = 0.f;
+      }
     } else if (brow) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
@@ -925,13 +979,15 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     float p[16];
     float bmax = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int t = t0 + 8 * (e >> 2) + 4 * hf + (e & 3);
-      float y = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
-      y = t < S ? y : -INFINITY;
-      p[e] = y;
-      bmax = fmaxf(bmax, y);
+    for (int e = 0; e < 16; ++e)
+      p[e] = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
+    if (t0 + kAttnK > S) {  // keys past the segment (uniform: the last block only)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (t0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= S) p[e] = -INFINITY;
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bmax = fmaxf(bmax, p[e]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
     const float m_new = fmaxf(m_run, bmax);
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;
@@ -983,6 +1039,19 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
         o[db] = mfma_h(ph, vhf, o[db]);
       }
     }
+  };
+  int blk = 0;
+  for (; blk + 2 < nblk; blk += 2) {
+    key_block(blk, std::true_type{}, std::false_type{});
+    __builtin_amdgcn_sched_barrier(0);  // one block's registers at a time
+    key_block(blk + 1, std::true_type{}, std::true_type{});
+  }
+  if (blk + 1 < nblk) {  // two blocks left (uniform)
+    key_block(blk, std::true_type{}, std::false_type{});
+    __builtin_amdgcn_sched_barrier(0);
+    key_block(blk + 1, std::false_type{}, std::true_type{});
+  } else {
+    key_block(blk, std::false_type{}, std::false_type{});
   }
   if (!live) return;
 
@@ -1069,9 +1138,9 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
     for (int i = 0; i < args.n_segs; ++i)
       if (args.segs[i].q_off % args.q_stride != 0) return hipErrorInvalidValue;
   }
-  // per-lane plane offsets are 32-bit
-  if ((uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
-      (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
+  // per-lane plane offsets are 32-bit, in bytes
+  if (2 * (uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
+      2 * (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
     return hipErrorInvalidValue;
   if (max_rows >= kLdsMinRows && kAttnWaves % args.group == 0) {
     // long segments: K/V blocks shared through LDS by 128 query-head rows
