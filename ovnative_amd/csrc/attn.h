@@ -44,13 +44,18 @@ hipError_t launch_qk_norm_rope(float* q, float* k, const float* qw, const float*
 hipError_t launch_attention(const AttnArgs& args, int max_rows, hipStream_t st);
 
 // Split-f16 attention (three f16 matrix-core products per fp32 product).
-// K and V are split once per call into f16 hi/lo planes:
-//   kh, kl : [T][kv_stride] row-major, the rows of k (same row indexing);
-//   vh, vl : [kv_heads*128][vt_cols] transposed, each segment's keys starting at
-//            column vt_off[s] (a multiple of 32, rows padded with zeros), keys
-//            permuted inside every 16-key group (bits 2 and 3 of the index
-//            swapped) and head-dim rows permuted (row 32j + r holds d = 4r + j)
-//            into the order the P.V matrix-core operands read them.
+// K and V are split once per call into f16 hi/lo planes, tile-major: each
+// segment's keys in 32-key blocks (padded with zeros; block index
+// kb = vt_off[s] / 32 + key / 32), and per (KV head kvh, block kb) 8 fragments
+// of 64 lanes x 8 halves at halves ((kvh * vt_cols/32 + kb) * 8 + f) * 512 +
+// lane * 8, each the 16 bytes one lane reads for one matrix-core operand:
+//   kh, kl : fragment f = 16-dim chunk, lane = key % 32 + 32 * ((d / 8) % 2),
+//            half = d % 8;
+//   vh, vl : head-dim rows permuted (row 32j + r holds d = 4r + j) and key
+//            positions permuted inside 16-key groups (bits 2 and 3 swapped);
+//            fragment f = 4 * (position / 16) + j, lane = r + 32 * ((position
+//            / 8) % 2), half = position % 8.
+// Each plane holds n_kv_heads * 128 * vt_cols halves;
 // vt_off[s] = sum over earlier segments of round_up(rows, 32).
 struct AttnSplit {
   _Float16* kh;
@@ -67,7 +72,7 @@ struct AttnSplit {
   int8_t* aq;
   float* asc;
 };
-// Splits K (the rows the segments cover) and V into the planes, then attends.
+// Splits K and V of the segments into the planes, then attends.
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                   hipStream_t st);
 // Attention alone, over planes already written (launch_qk_norm_rope_split); the
@@ -77,8 +82,8 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
 // uint8 mask [rows, rows] (non-zero = visible) -> AttnSeg::bits words.
 hipError_t launch_mask_bits(const uint8_t* mask, int rows, uint32_t* bits, hipStream_t st);
 // launch_qk_norm_rope (D = 128) that also writes the planes of the roped k rows
-// (sp.kh/kl at k's indexing, args.kv_stride = n_kv_heads * 128) and of the V
-// tiles of args' segments, in one launch.
+// of args' segments (args.kv_stride = n_kv_heads * 128) and of their V, in one
+// launch.
 hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const float* kw,
                                      int64_t rows, int n_heads, int n_kv_heads,
                                      const float* cos_tab, const float* sin_tab, float eps,

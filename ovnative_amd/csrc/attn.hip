@@ -319,6 +319,7 @@ hipError_t launch_attention(const AttnArgs& args, int max_rows, hipStream_t st) 
 // pass reports them through `overflow` (the reference's own GPU path runs its
 // activations in fp16 too, cuda_lm.cu:1086-1160).
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void split16(float x, _Float16& hi, _Float16& lo) {
   hi = (_Float16)x;
@@ -330,35 +331,52 @@ __device__ __forceinline__ f32x16 mfma_h(h8 a, h8 b, f32x16 c) {
 }
 
 // ---- f16 hi/lo planes of K and V --------------------------------------------
-// K: element i of the k rows -> kh[i], kl[i] (same row indexing and stride).
-__device__ __forceinline__ bool split_k8(const float* __restrict__ src, _Float16* __restrict__ dh,
-                                         _Float16* __restrict__ dl) {
-  const f32x4 x0 = *reinterpret_cast<const f32x4*>(src);
-  const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + 4);
-  h8 h, l;
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float x = j < 4 ? x0[j] : x1[j - 4];
-    bad |= !(fabsf(x) < 65504.f);
-    _Float16 a, b;
-    split16(x, a, b);
-    h[j] = a;
-    l[j] = b;
-  }
-  *reinterpret_cast<h8*>(dh) = h;
-  *reinterpret_cast<h8*>(dl) = l;
-  return bad;
+// Tile-major (see AttnSplit): per (KV head, 32-key block) 8 fragments of 64
+// lanes x 8 halves, each the 16 bytes one lane reads for one matrix-core
+// operand, so a wavefront's fragment load is 1 KiB of contiguous memory.
+constexpr int kTileHalves = 8 * 64 * 8;  // per (KV head, key block) and plane
+
+// K: key kk of block kb, dim d -> fragment d/16, lane kk + 32*((d/8)%2), half d%8.
+__device__ __forceinline__ int64_t k_tile_index(int kvh, int64_t nkb, int64_t kb, int kk, int d) {
+  return ((((int64_t)kvh * nkb + kb) * 8 + (d >> 4)) * 64 + kk + 32 * ((d >> 3) & 1)) * 8 + (d & 7);
 }
 
-// V: one 32-key x 32-dim tile (key tile `kt` of segment `s`, dims 32*dq..+31 of
-// KV head `kvh`) through LDS.  Output row 32j + r of a head holds d = 4r + j;
-// column vt_off[s] + key with bits 2 and 3 swapped; keys past the segment are 0.
-// `tile` is 32 x 33 floats of LDS.  Returns true when a value is beyond f16.
+// V (and K) of one 32-key x 32-dim tile (key tile `kt` of segment `s`, dims
+// 32*dq..+31 of KV head `kvh`).  V goes through LDS: head-dim row 32j + r holds
+// d = 4r + j, stored key position m holds key m with bits 2 and 3 swapped, and
+// fragment 4*(m/16) + j, lane r + 32*((m/8)%2) of the block holds the 8 keys
+// of that lane; keys past the segment are 0.  K: with `write_k` the tile's k
+// values, otherwise only zeros for keys past the segment (the real keys come
+// from the qk-norm/RoPE wavefronts).  `tile` is 32 x 33 floats of LDS.
+// Returns true when a value is beyond f16.
 __device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit& sp, int s, int kt,
-                                             int kvh, int dq, float (*tile)[33]) {
+                                             int kvh, int dq, float (*tile)[33], bool write_k) {
   const AttnSeg seg = a.segs[s];
   const int t0 = kt * 32;
+  const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[s] / 32 + kt;
+  bool bad = false;
+  {
+    const int key = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
+    const bool real = t0 + key < seg.rows;
+    if (write_k || !real) {
+      f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (real)
+        x = *reinterpret_cast<const f32x4*>(a.k + seg.kv_off + (int64_t)(t0 + key) * a.kv_stride +
+                                            kvh * kAttnD + dq * 32 + c4);
+      h4 hh, ll;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bad |= !(fabsf(x[j]) < 65504.f);
+        _Float16 hi, lo;
+        split16(x[j], hi, lo);
+        hh[j] = hi;
+        ll[j] = lo;
+      }
+      const int64_t ki = k_tile_index(kvh, nkb, kb, key, dq * 32 + c4);
+      *reinterpret_cast<h4*>(sp.kh + ki) = hh;
+      *reinterpret_cast<h4*>(sp.kl + ki) = ll;
+    }
+  }
   {
     const int key = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
     f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -369,7 +387,6 @@ __device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit&
     for (int j = 0; j < 4; ++j) tile[key][c4 + j] = x[j];
   }
   __syncthreads();
-  bool bad = false;
   if (threadIdx.x < 128) {
     const int dl = threadIdx.x >> 2, kg = threadIdx.x & 3;
     const int d = dq * 32 + dl;
@@ -385,45 +402,31 @@ __device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit&
       h[i] = hi;
       l[i] = lo;
     }
-    const int64_t orow = (int64_t)kvh * kAttnD + 32 * (d & 3) + (d >> 2);
-    const int64_t col = sp.vt_off[s] + t0 + 8 * kg;
-    *reinterpret_cast<h8*>(sp.vh + orow * sp.vt_cols + col) = h;
-    *reinterpret_cast<h8*>(sp.vl + orow * sp.vt_cols + col) = l;
+    const int64_t vi =
+        ((((int64_t)kvh * nkb + kb) * 8 + 4 * (kg >> 1) + (d & 3)) * 64 + (d >> 2) + 32 * (kg & 1)) * 8;
+    *reinterpret_cast<h8*>(sp.vh + vi) = h;
+    *reinterpret_cast<h8*>(sp.vl + vi) = l;
   }
   return bad;
 }
 
 // V tiles of one launch: blockIdx -> (segment, key tile, kv head, dim quarter).
 __device__ __forceinline__ bool split_v_job(const AttnArgs& a, const AttnSplit& sp, int64_t job,
-                                            int ktiles, float (*tile)[33]) {
+                                            int ktiles, float (*tile)[33], bool write_k) {
   const int per_seg = ktiles * sp.n_kv_heads * 4;
   const int s = (int)(job / per_seg);
   int r = (int)(job - (int64_t)s * per_seg);
   const int kt = r / (sp.n_kv_heads * 4);
   r -= kt * sp.n_kv_heads * 4;
   if (kt * 32 >= a.segs[s].rows) return false;  // uniform for the workgroup
-  return split_v_tile(a, sp, s, kt, r >> 2, r & 3, tile);
+  return split_v_tile(a, sp, s, kt, r >> 2, r & 3, tile, write_k);
 }
 
-// Standalone split of K (rows [r_lo, r_lo + k_rows)) and V for one attention call:
-// the first k_blocks workgroups take 2048 K elements each, the rest one V tile.
-__global__ __launch_bounds__(256) void split_kv_kernel(AttnArgs a, AttnSplit sp, int64_t r_lo,
-                                                       int64_t k_rows, int64_t k_blocks,
-                                                       int ktiles) {
+// Standalone split of K and V for one attention call: one workgroup per
+// (segment, key tile, KV head, dim quarter).
+__global__ __launch_bounds__(256) void split_kv_kernel(AttnArgs a, AttnSplit sp, int ktiles) {
   __shared__ float tile[32][33];
-  bool bad = false;
-  if ((int64_t)blockIdx.x < k_blocks) {
-    const int64_t width = (int64_t)sp.n_kv_heads * kAttnD;
-    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-    const int64_t r = i / width, c = i - r * width;
-    if (r < k_rows) {
-      const int64_t off = (r_lo + r) * a.kv_stride + c;
-      bad = split_k8(a.k + off, sp.kh + off, sp.kl + off);
-    }
-  } else {
-    bad = split_v_job(a, sp, (int64_t)blockIdx.x - k_blocks, ktiles, tile);
-  }
-  if (bad) atomicOr(sp.overflow, 1u);
+  if (split_v_job(a, sp, (int64_t)blockIdx.x, ktiles, tile, true)) atomicOr(sp.overflow, 1u);
 }
 
 // The runner's form: per-head RMSNorm + RoPE of q and k (as qk_norm_rope_kernel,
@@ -436,7 +439,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
     int64_t qk_blocks, int ktiles, AttnArgs a, AttnSplit sp) {
   __shared__ float tile[32][33];
   if ((int64_t)blockIdx.x >= qk_blocks) {
-    if (split_v_job(a, sp, (int64_t)blockIdx.x - qk_blocks, ktiles, tile))
+    if (split_v_job(a, sp, (int64_t)blockIdx.x - qk_blocks, ktiles, tile, false))
       atomicOr(sp.overflow, 1u);
     return;
   }
@@ -456,13 +459,29 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
   v[lane] = oa;
   v[lane + half] = ob;
   if (is_k) {
+    // the segment of row r (uniform for the wavefront) and its key block
+    int sidx = -1;
+    int64_t t = 0;
+    for (int i = 0; i < a.n_segs; ++i) {
+      const int64_t r0 = a.segs[i].kv_off / a.kv_stride;
+      if (r >= r0 && r < r0 + a.segs[i].rows) {
+        sidx = i;
+        t = r - r0;
+      }
+    }
+    if (sidx < 0) return;
+    const int kvh = h - n_heads;
+    const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[sidx] / 32 + t / 32;
+    const int kk = (int)(t & 31);
     _Float16 h0, l0, h1, l1;
     split16(oa, h0, l0);
     split16(ob, h1, l1);
-    sp.kh[off + lane] = h0;
-    sp.kl[off + lane] = l0;
-    sp.kh[off + lane + half] = h1;
-    sp.kl[off + lane + half] = l1;
+    const int64_t i0 = k_tile_index(kvh, nkb, kb, kk, lane);
+    const int64_t i1 = k_tile_index(kvh, nkb, kb, kk, lane + half);
+    sp.kh[i0] = h0;
+    sp.kl[i0] = l0;
+    sp.kh[i1] = h1;
+    sp.kl[i1] = l1;
     if (!(fabsf(oa) < 65504.f) || !(fabsf(ob) < 65504.f)) atomicOr(sp.overflow, 1u);
   }
 }
@@ -533,17 +552,14 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     }
   }
 
-  // Wave-uniform plane bases and 32-bit per-lane byte offsets (the launcher
-  // checks that every offset fits), so the loads take a scalar base.
-  const int64_t krow0 = seg.kv_off / args.kv_stride;  // segment's first k row
-  const _Float16* __restrict__ khb = sp.kh + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
-  const _Float16* __restrict__ klb = sp.kl + krow0 * args.kv_stride + (int64_t)kvh * kAttnD;
-  const int64_t vbase = (int64_t)kvh * kAttnD * sp.vt_cols + sp.vt_off[sidx];
-  const _Float16* __restrict__ vhb = sp.vh + vbase;
-  const _Float16* __restrict__ vlb = sp.vl + vbase;
-  const uint32_t vlane = (uint32_t)(r32 * sp.vt_cols + 8 * hf);
-  const uint32_t vstep = 32u * (uint32_t)sp.vt_cols;  // 32 head-dim rows of the V planes
-  const uint32_t kstride = (uint32_t)args.kv_stride;
+  // Wave-uniform bases of this (KV head, segment)'s tiles and 32-bit per-lane
+  // byte offsets (the launcher checks that every offset fits), so the loads
+  // take a scalar base; fragment j of key block b is 1 KiB at (8b + j) KiB.
+  const int64_t tiles0 = ((int64_t)kvh * (sp.vt_cols / 32) + sp.vt_off[sidx] / 32) * kTileHalves;
+  const _Float16* __restrict__ khb = sp.kh + tiles0;
+  const _Float16* __restrict__ klb = sp.kl + tiles0;
+  const _Float16* __restrict__ vhb = sp.vh + tiles0;
+  const _Float16* __restrict__ vlb = sp.vl + tiles0;
 
   // Mask of this lane's query row: bit words (kBits) or the additive bias row.
   // Without mask words every block reads the one all-visible word, so the
@@ -566,22 +582,20 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     return *reinterpret_cast<const h8*>(reinterpret_cast<const char*>(base) + 2u * elem);
   };
   auto load_k = [&](int t0) {
-    const uint32_t off = (uint32_t)min(t0 + r32, S - 1) * kstride + 8 * hf;
+    const uint32_t off = (uint32_t)(t0 >> 5) * kTileHalves + 8u * (uint32_t)lane;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      kh[c] = ld(khb, off + 16 * c);
-      kl[c] = ld(klb, off + 16 * c);
+      kh[c] = ld(khb, off + 512 * c);
+      kl[c] = ld(klb, off + 512 * c);
     }
   };
   auto load_v = [&](int t0) {
+    const uint32_t off = (uint32_t)(t0 >> 5) * kTileHalves + 8u * (uint32_t)lane;
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint32_t off = vlane + db * vstep + (uint32_t)(t0 + 16 * c);
-        vh[4 * c + db] = ld(vhb, off);
-        vl[4 * c + db] = ld(vlb, off);
-      }
+    for (int j = 0; j < 8; ++j) {  // j = 4 * (16-key chunk) + head-dim block
+      vh[j] = ld(vhb, off + 512 * j);
+      vl[j] = ld(vlb, off + 512 * j);
+    }
   };
 
   f32x16 o[4];
@@ -828,10 +842,12 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // V [128 rows][4 chunks of 8 keys] (the rows and key order of the global V
 // planes), chunk slot = c ^ ((row >> 2) & 3).
 constexpr int kLdsPlane = 32 * kAttnD;  // halves per plane per block
-// Longest segment from which this form is used: measured with 2 segments of S
-// rows, 16/8 heads (short form vs this, us): S = 512: 39.8 vs 45.6, 768: 81.8
-// vs 66.3, 1024: 138.6 vs 90.8.
+// The long-sequence form pays once segments are long and its workgroups fill
+// the chip (MI355X: 16 x 1024 rows 41.6 vs 42.7 ms per LM forward with the
+// form above); with few segments the form above has 4x the workgroups and
+// wins (2 x 1024 rows: 74 vs 82 us).
 constexpr int kLdsMinRows = 640;
+constexpr int kLdsMinTasks = 512;
 
 template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs args, AttnSplit sp,
@@ -888,22 +904,21 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
   // ---- DMA sources.  Wave w moves plane w of each block (8 x 1 KiB):
   // K planes (w < 2): slot s = 64 i + lane -> key s/16, chunk (s%16) ^ (key&15);
   // V planes: slot s -> row s/4, chunk (s%4) ^ ((row>>2)&3).
-  const int64_t krow0 = seg.kv_off / args.kv_stride;
-  const _Float16* plane = wave == 0 ? sp.kh : wave == 1 ? sp.kl : wave == 2 ? sp.vh : sp.vl;
+  const _Float16* plane = (wave == 0 ? sp.kh : wave == 1 ? sp.kl : wave == 2 ? sp.vh : sp.vl) +
+                          ((int64_t)kvh * (sp.vt_cols / 32) + sp.vt_off[sidx] / 32) * kTileHalves;
   auto issue = [&](int blk, auto odd) __attribute__((always_inline)) {
-    const int t0 = blk * kAttnK;
+    const _Float16* pb = plane + (int64_t)blk * kTileHalves;  // the block's tiles
     _Float16* dst = decltype(odd)::value ? &kv1[wave][0] : &kv0[wave][0];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int s = 64 * i + lane;
       const _Float16* src;
-      if (wave < 2) {
+      if (wave < 2) {  // 8 dims c of key `key`: fragment c/2, lane key + 32*(c%2)
         const int key = s >> 4, c = (s & 15) ^ (key & 15);
-        const int kr = min(t0 + key, S - 1);
-        src = plane + (krow0 + kr) * args.kv_stride + (int64_t)kvh * kAttnD + 8 * c;
-      } else {
+        src = pb + ((c >> 1) * 64 + key + 32 * (c & 1)) * 8;
+      } else {  // 8 stored key positions 8c.. of head-dim row `row`
         const int row = s >> 2, c = (s & 3) ^ ((row >> 2) & 3);
-        src = plane + ((int64_t)kvh * kAttnD + row) * sp.vt_cols + sp.vt_off[sidx] + t0 + 8 * c;
+        src = pb + ((4 * (c >> 1) + (row >> 5)) * 64 + (row & 31) + 32 * (c & 1)) * 8;
       }
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
                                        (lds_void_t*)(dst + 512 * i), 16, 0, 0);
@@ -1109,21 +1124,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                   hipStream_t st) {
   if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
-  // K: the rows the segments cover, as one range [first row, last row]
-  int64_t r_lo = INT64_MAX, r_hi = 0;
-  for (int i = 0; i < args.n_segs; ++i) {
-    if (args.segs[i].rows <= 0) continue;
-    const int64_t r0 = args.segs[i].kv_off / args.kv_stride;
-    r_lo = r0 < r_lo ? r0 : r_lo;
-    r_hi = r0 + args.segs[i].rows > r_hi ? r0 + args.segs[i].rows : r_hi;
-  }
-  if (r_hi <= r_lo) return hipSuccess;
-  const int64_t width = (int64_t)sp.n_kv_heads * kAttnD;
-  const int64_t k_blocks = ((r_hi - r_lo) * width / 8 + 255) / 256;
   const int ktiles = (max_rows + 31) / 32;
-  const int64_t v_jobs = (int64_t)args.n_segs * ktiles * sp.n_kv_heads * 4;
-  hipLaunchKernelGGL(split_kv_kernel, dim3((unsigned)(k_blocks + v_jobs)), dim3(256), 0, st, args,
-                     sp, r_lo, r_hi - r_lo, k_blocks, ktiles);
+  const int64_t jobs = (int64_t)args.n_segs * ktiles * sp.n_kv_heads * 4;
+  hipLaunchKernelGGL(split_kv_kernel, dim3((unsigned)jobs), dim3(256), 0, st, args, sp, ktiles);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_attention_split_only(args, sp, max_rows, false, st);
@@ -1138,15 +1141,17 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
     for (int i = 0; i < args.n_segs; ++i)
       if (args.segs[i].q_off % args.q_stride != 0) return hipErrorInvalidValue;
   }
-  // per-lane plane offsets are 32-bit, in bytes
-  if (2 * (uint64_t)max_rows * (uint64_t)args.kv_stride >= (1ull << 32) ||
-      2 * (uint64_t)kAttnD * (uint64_t)sp.vt_cols >= (1ull << 32))
-    return hipErrorInvalidValue;
-  if (max_rows >= kLdsMinRows && kAttnWaves % args.group == 0) {
-    // long segments: K/V blocks shared through LDS by 128 query-head rows
-    const int QT = kAttnWaves * kAttnQ / args.group;
-    const int qtiles = (max_rows + QT - 1) / QT;
-    const int tasks = args.n_segs * (args.n_heads / args.group) * qtiles;
+  // per-lane offsets into one KV head's tiles are 32-bit, in bytes
+  // (vt_cols / 32 blocks x 8 KiB)
+  if (256 * (uint64_t)sp.vt_cols >= (1ull << 32) || sp.vt_cols % 32 != 0) return hipErrorInvalidValue;
+  const int QT = kAttnWaves * kAttnQ / args.group;  // query rows per long-form workgroup
+  const int lds_qtiles = (max_rows + QT - 1) / QT;
+  const int lds_tasks = args.n_segs * (args.n_heads / args.group) * lds_qtiles;
+  if (max_rows >= kLdsMinRows && lds_tasks >= kLdsMinTasks && kAttnWaves % args.group == 0) {
+    // long segments, many of them: K/V blocks shared through LDS by 128
+    // query-head rows
+    const int qtiles = lds_qtiles;
+    const int tasks = lds_tasks;
     const int per_xcd = (tasks + 7) / 8;
     const dim3 grid((unsigned)(8 * per_xcd));
     if (mask_bits)

@@ -447,7 +447,6 @@ int ovh_attention_split(const OvhAttnSegment* segs, int n_segs, int n_heads, int
   a.n_heads = n_heads; a.group = n_heads / n_kv_heads; a.scale = scale; a.n_segs = n_segs;
   ovh::AttnSplit sp{};
   int max_rows = 0;
-  int64_t rows_hi = 0;
   for (int s = 0; s < n_segs; ++s) {
     const OvhAttnSegment& g = segs[s];
     if (g.rows < 0 || g.q_off < 0 || g.kv_off < 0 || (g.q_off & 7) || g.kv_off % kv_stride)
@@ -457,13 +456,11 @@ int ovh_attention_split(const OvhAttnSegment* segs, int n_segs, int n_heads, int
     sp.vt_off[s] = sp.vt_cols;
     sp.vt_cols += (g.rows + 31) / 32 * 32;
     max_rows = g.rows > max_rows ? g.rows : max_rows;
-    const int64_t end = g.kv_off / kv_stride + g.rows;
-    rows_hi = end > rows_hi ? end : rows_hi;
   }
   sp.n_kv_heads = n_kv_heads;
   hipStream_t st = as_stream(stream);
-  const size_t kbytes = sizeof(_Float16) * (size_t)(rows_hi * kv_stride);
   const size_t vbytes = sizeof(_Float16) * (size_t)((int64_t)n_kv_heads * head_dim * sp.vt_cols);
+  const size_t kbytes = vbytes;  // K and V planes are both tile-major over the padded keys
   char* ws = nullptr;
   const size_t total = 2 * kbytes + 2 * vbytes + 256;
   OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), total, st), "hipMallocAsync(split)");

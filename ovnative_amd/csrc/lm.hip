@@ -573,15 +573,15 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
             b_v = take(sizeof(float) * (size_t)(T * KVD)), b_at = take(sizeof(float) * (size_t)(T * QD)),
             b_g = take(sizeof(float) * (size_t)(T * I)), b_u = take(sizeof(float) * (size_t)(T * I)),
             b_lg = take(sizeof(float) * (size_t)(T * CV));
-  // split-f16 attention planes (k rows as stored; V transposed, segments padded to 32)
+  // split-f16 attention planes (K and V tile-major, segments padded to 32 keys)
   int64_t vt_cols = 0;
   std::vector<int64_t> vt_off(segs.size());
   for (size_t i = 0; i < segs.size(); ++i) {
     vt_off[i] = vt_cols;
     vt_cols += (segs[i].rows + 31) / 32 * 32;
   }
-  const Buf b_kh = take(split ? sizeof(_Float16) * (size_t)(T * KVD) : 0),
-            b_kl = take(split ? sizeof(_Float16) * (size_t)(T * KVD) : 0),
+  const Buf b_kh = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0),
+            b_kl = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0),
             b_vh = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0),
             b_vl = take(split ? sizeof(_Float16) * (size_t)(KVD * vt_cols) : 0);
   if (cur > L.arena_cap) {

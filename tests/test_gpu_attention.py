@@ -130,7 +130,8 @@ def _segments(rng, seg_rows, masked):
     ([300, 300], 16, 8, False),   # BASELINE config 3/4: CFG batch 2, seq 300
     ([300, 260], 16, 8, True),    # ragged CFG (cond S, uncond T) with masks
     ([1024], 16, 8, False),       # one sequence of config 5
-    ([700, 650], 16, 8, True),    # long segments, masked (split form: LDS-shared K/V)
+    ([700, 650], 16, 8, True),    # long segments, masked
+    ([700] * 11, 16, 8, True),    # many long segments (split: the LDS-shared K/V form)
     ([640, 3], 8, 2, True),       # KV group of 4, a segment shorter than the tile
     ([700], 4, 4, False),         # KV group of 1
     ([1, 33, 64, 65], 4, 2, True),
