@@ -837,10 +837,9 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // buffered) and read by all four, and every wavefront walks all keys itself, so
 // there is no merge.  Per element the arithmetic is the form above's (three f16
 // products, base-2 online softmax, same masks, same quantised epilogue).
-// LDS planes of a block, 16-byte chunks XOR-swizzled so the fragment reads are
-// conflict-free: K [32 keys][16 chunks of 8 d], chunk slot = c ^ (key & 15);
-// V [128 rows][4 chunks of 8 keys] (the rows and key order of the global V
-// planes), chunk slot = c ^ ((row >> 2) & 3).
+// LDS planes of a block: the block's 8 fragments of each global plane as they
+// are stored (1 KiB each, lane-linear), so the DMA copies them verbatim and a
+// wavefront's fragment read is 64 contiguous 16-byte slots (conflict-free).
 constexpr int kLdsPlane = 32 * kAttnD;  // halves per plane per block
 // The long-sequence form pays once segments are long and its workgroups fill
 // the chip (MI355X: 16 x 1024 rows 41.6 vs 42.7 ms per LM forward with the
@@ -910,19 +909,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     const _Float16* pb = plane + (int64_t)blk * kTileHalves;  // the block's tiles
     _Float16* dst = decltype(odd)::value ? &kv1[wave][0] : &kv0[wave][0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int s = 64 * i + lane;
-      const _Float16* src;
-      if (wave < 2) {  // 8 dims c of key `key`: fragment c/2, lane key + 32*(c%2)
-        const int key = s >> 4, c = (s & 15) ^ (key & 15);
-        src = pb + ((c >> 1) * 64 + key + 32 * (c & 1)) * 8;
-      } else {  // 8 stored key positions 8c.. of head-dim row `row`
-        const int row = s >> 2, c = (s & 3) ^ ((row >> 2) & 3);
-        src = pb + ((4 * (c >> 1) + (row >> 5)) * 64 + (row & 31) + 32 * (c & 1)) * 8;
-      }
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+    for (int i = 0; i < 8; ++i)  // fragment i of this wavefront's plane
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(pb + 512 * i + 8 * lane),
                                        (lds_void_t*)(dst + 512 * i), 16, 0, 0);
-    }
   };
 
   // mask words as in attention_split_kernel: the all-visible word when the
@@ -943,7 +932,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[c][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
-  const int kslot = r32 * kAttnD;  // this lane's key row in a K plane
+  const int lslot = 8 * lane;  // this lane's 16 bytes in an LDS fragment
 
   // The last block is peeled off as the one that issues no DMA, so no load
   // sits under a branch inside the loop.
@@ -967,7 +956,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const int off = kslot + 8 * ((2 * c + hf) ^ (r32 & 15));
+      const int off = 512 * c + lslot;
       const h8 khf = *reinterpret_cast<const h8*>(kb + off);
       const h8 klf = *reinterpret_cast<const h8*>(kb + kLdsPlane + off);
       st = mfma_h(klf, qh[c], st);
@@ -1045,8 +1034,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
       }
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int row = 32 * db + r32;
-        const int off = row * kAttnK + 8 * ((2 * c + hf) ^ ((row >> 2) & 3));
+        const int off = 512 * (4 * c + db) + lslot;
         const h8 vhf = *reinterpret_cast<const h8*>(vb + off);
         const h8 vlf = *reinterpret_cast<const h8*>(vb + kLdsPlane + off);
         o[db] = mfma_h(pl, vhf, o[db]);
