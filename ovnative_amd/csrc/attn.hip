@@ -350,7 +350,8 @@ __device__ __forceinline__ int64_t k_tile_index(int kvh, int64_t nkb, int64_t kb
 // from the qk-norm/RoPE wavefronts).  `tile` is 32 x 33 floats of LDS.
 // Returns true when a value is beyond f16.
 __device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit& sp, int s, int kt,
-                                             int kvh, int dq, float (*tile)[33], bool write_k) {
+                                             int kvh, int dq, float (*tile)[33], bool write_k,
+                                             bool k_pad = true) {
   const AttnSeg seg = a.segs[s];
   const int t0 = kt * 32;
   const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[s] / 32 + kt;
@@ -358,7 +359,7 @@ __device__ __forceinline__ bool split_v_tile(const AttnArgs& a, const AttnSplit&
   {
     const int key = threadIdx.x >> 3, c4 = (threadIdx.x & 7) * 4;
     const bool real = t0 + key < seg.rows;
-    if (write_k || !real) {
+    if (write_k || (k_pad && !real)) {
       f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
       if (real)
         x = *reinterpret_cast<const f32x4*>(a.k + seg.kv_off + (int64_t)(t0 + key) * a.kv_stride +
@@ -429,61 +430,118 @@ __global__ __launch_bounds__(256) void split_kv_kernel(AttnArgs a, AttnSplit sp,
   if (split_v_job(a, sp, (int64_t)blockIdx.x, ktiles, tile, true)) atomicOr(sp.overflow, 1u);
 }
 
-// The runner's form: per-head RMSNorm + RoPE of q and k (as qk_norm_rope_kernel,
-// one wavefront per (row, head)) that also writes the f16 planes of the roped k,
-// and, in the workgroups past the q/k ones, the V tiles.
-__global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
-    float* __restrict__ q, float* __restrict__ k, const float* __restrict__ qw,
-    const float* __restrict__ kw, int64_t rows, int n_heads, int n_kv_heads,
-    const float* __restrict__ cos_tab, const float* __restrict__ sin_tab, float eps,
-    int64_t qk_blocks, int ktiles, AttnArgs a, AttnSplit sp) {
-  __shared__ float tile[32][33];
-  if ((int64_t)blockIdx.x >= qk_blocks) {
-    if (split_v_job(a, sp, (int64_t)blockIdx.x - qk_blocks, ktiles, tile, false))
-      atomicOr(sp.overflow, 1u);
-    return;
-  }
+// The same RMSNorm + RoPE with 8 lanes per head vector: lane j of the group
+// holds x[j + 8i], i = 0..15 (D = 128), i.e. the reference's fma chain j, and
+// both members of the rotation pairs (j + 8i, j + 8i + 64), i < 8.  The chain
+// runs in registers, the 8 chain sums are added left to right after 7 lane
+// reads, and every value is the one norm_rope_pair computes.
+__device__ __forceinline__ void norm_rope_lanes8(float (&x)[16], const float* __restrict__ w,
+                                                 const float* __restrict__ cos_row,
+                                                 const float* __restrict__ sin_row, float eps,
+                                                 int j) {
   constexpr int D = kAttnD, half = D / 2;
-  const int lane = threadIdx.x & 63;
-  const int heads = n_heads + n_kv_heads;
-  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (task >= rows * heads) return;
-  const int64_t r = task / heads;
-  const int h = (int)(task - r * heads);
-  const bool is_k = h >= n_heads;
-  const int64_t off = is_k ? (r * n_kv_heads + (h - n_heads)) * D : (r * n_heads + h) * D;
-  float* v = (is_k ? k : q) + off;
-  float oa, ob;
-  if (!norm_rope_pair<D>(v, is_k ? kw : qw, cos_tab + r * half, sin_tab + r * half, eps, lane, oa, ob))
-    return;
-  v[lane] = oa;
-  v[lane + half] = ob;
-  if (is_k) {
-    // the segment of row r (uniform for the wavefront) and its key block
-    int sidx = -1;
-    int64_t t = 0;
-    for (int i = 0; i < a.n_segs; ++i) {
-      const int64_t r0 = a.segs[i].kv_off / a.kv_stride;
-      if (r >= r0 && r < r0 + a.segs[i].rows) {
-        sidx = i;
-        t = r - r0;
-      }
-    }
-    if (sidx < 0) return;
-    const int kvh = h - n_heads;
-    const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[sidx] / 32 + t / 32;
-    const int kk = (int)(t & 31);
-    _Float16 h0, l0, h1, l1;
-    split16(oa, h0, l0);
-    split16(ob, h1, l1);
-    const int64_t i0 = k_tile_index(kvh, nkb, kb, kk, lane);
-    const int64_t i1 = k_tile_index(kvh, nkb, kb, kk, lane + half);
-    sp.kh[i0] = h0;
-    sp.kl[i0] = l0;
-    sp.kh[i1] = h1;
-    sp.kl[i1] = l1;
-    if (!(fabsf(oa) < 65504.f) || !(fabsf(ob) < 65504.f)) atomicOr(sp.overflow, 1u);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = fmaf(x[i], x[i], s);
+  const int g0 = (threadIdx.x & 63) & ~7;  // the group's first lane
+  float sum = __shfl(s, g0);
+#pragma unroll
+  for (int c = 1; c < 8; ++c) sum = __fadd_rn(sum, __shfl(s, g0 + c));
+  const float scale = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)D), eps)));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = j + 8 * i;
+    const float c = cos_row[d], sn = sin_row[d];
+    const float na = __fmul_rn(__fmul_rn(x[i], scale), w[d]);
+    const float nb = __fmul_rn(__fmul_rn(x[i + 8], scale), w[d + half]);
+    x[i] = fmaf(na, c, -__fmul_rn(nb, sn));
+    x[i + 8] = fmaf(na, sn, __fmul_rn(nb, c));
   }
+}
+
+// The runner's form of qk-norm + RoPE + plane split, in one launch.  The first
+// q_blocks workgroups: q in place, 32 (row, head) vectors per workgroup, 8
+// lanes each.  The rest: one workgroup per (segment, 32-key tile, KV head):
+// the tile's k rows normalised and rotated the same way (8 lanes per key),
+// staged in LDS and written to the K planes 16 bytes per slot (keys past the
+// segment as zeros), then the tile's V in four 32-dim passes.
+__global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
+    float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ qw,
+    const float* __restrict__ kw, int64_t rows, int n_heads, const float* __restrict__ cos_tab,
+    const float* __restrict__ sin_tab, float eps, int64_t q_blocks, int ktiles, AttnArgs a,
+    AttnSplit sp) {
+  constexpr int D = kAttnD, half = D / 2;
+  __shared__ float tile[32][33];
+  __shared__ float kt_s[32][D + 4];  // one key tile, normalised and rotated
+  const int j = threadIdx.x & 7;
+  if ((int64_t)blockIdx.x < q_blocks) {
+    const int64_t task = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    if (task >= rows * n_heads) return;  // whole 8-lane groups leave together
+    const int64_t r = task / n_heads;
+    float* v = q + task * D;  // q rows are n_heads * D wide
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = v[j + 8 * i];
+    norm_rope_lanes8(x, qw, cos_tab + r * half, sin_tab + r * half, eps, j);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[j + 8 * i] = x[i];
+    return;
+  }
+  // (segment, key tile, KV head)
+  const int64_t job = (int64_t)blockIdx.x - q_blocks;
+  const int per_seg = ktiles * sp.n_kv_heads;
+  const int s = (int)(job / per_seg);
+  const int rem = (int)(job - (int64_t)s * per_seg);
+  const int ktile = rem / sp.n_kv_heads, kvh = rem - ktile * sp.n_kv_heads;
+  const AttnSeg seg = a.segs[s];
+  const int t0 = ktile * 32;
+  if (t0 >= seg.rows) return;  // uniform for the workgroup
+  const int64_t r0 = seg.kv_off / a.kv_stride;  // the segment's first k row
+  bool bad = false;
+  {
+    const int key = threadIdx.x >> 3;
+    float x[16];
+    if (t0 + key < seg.rows) {
+      const int64_t r = r0 + t0 + key;
+      const float* kr = k + r * a.kv_stride + (int64_t)kvh * D;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = kr[j + 8 * i];
+      norm_rope_lanes8(x, kw, cos_tab + r * half, sin_tab + r * half, eps, j);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kt_s[key][j + 8 * i] = x[i];
+  }
+  __syncthreads();
+  {
+    // slots: (key, 8-dim group g) -> fragment g/2, lane key + 32*(g%2)
+    const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[s] / 32 + ktile;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int slot = threadIdx.x + 256 * u, key = slot & 31, g = slot >> 5;
+      h8 hh, ll;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xv = kt_s[key][8 * g + e];
+        bad |= !(fabsf(xv) < 65504.f);
+        _Float16 hi, lo;
+        split16(xv, hi, lo);
+        hh[e] = hi;
+        ll[e] = lo;
+      }
+      const int64_t ki = k_tile_index(kvh, nkb, kb, key, 8 * g);
+      *reinterpret_cast<h8*>(sp.kh + ki) = hh;
+      *reinterpret_cast<h8*>(sp.kl + ki) = ll;
+    }
+  }
+#pragma unroll 1
+  for (int dq = 0; dq < 4; ++dq) {
+    __syncthreads();  // `tile` is reused by each pass
+    bad |= split_v_tile(a, sp, s, ktile, kvh, dq, tile, false, false);
+  }
+  if (bad) atomicOr(sp.overflow, 1u);
 }
 
 // Attention over the planes.  Same work split as attention_kernel (one
@@ -1192,14 +1250,15 @@ hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const 
                                      const float* cos_tab, const float* sin_tab, float eps,
                                      const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                      hipStream_t st) {
-  const int64_t tasks = rows * (n_heads + n_kv_heads);
-  if (tasks <= 0) return hipSuccess;
-  const int64_t qk_blocks = (tasks + 3) / 4;
+  if (rows <= 0) return hipSuccess;
+  if (args.kv_stride != (int64_t)n_kv_heads * kAttnD || sp.n_kv_heads != n_kv_heads)
+    return hipErrorInvalidValue;
+  const int64_t q_blocks = (rows * n_heads + 31) / 32;
   const int ktiles = (max_rows + 31) / 32;
-  const int64_t v_jobs = args.n_segs > 0 ? (int64_t)args.n_segs * ktiles * sp.n_kv_heads * 4 : 0;
-  hipLaunchKernelGGL(qk_norm_rope_split_kernel, dim3((unsigned)(qk_blocks + v_jobs)), dim3(256), 0,
-                     st, q, k, qw, kw, rows, n_heads, n_kv_heads, cos_tab, sin_tab, eps, qk_blocks,
-                     ktiles, args, sp);
+  const int64_t kv_jobs = args.n_segs > 0 ? (int64_t)args.n_segs * ktiles * n_kv_heads : 0;
+  hipLaunchKernelGGL(qk_norm_rope_split_kernel, dim3((unsigned)(q_blocks + kv_jobs)), dim3(256), 0,
+                     st, q, k, qw, kw, rows, n_heads, cos_tab, sin_tab, eps, q_blocks, ktiles,
+                     args, sp);
   return hipGetLastError();
 }
 
