@@ -461,10 +461,10 @@ __device__ __forceinline__ void norm_rope_lanes8(float (&x)[16], const float* __
 
 // The runner's form of qk-norm + RoPE + plane split, in one launch.  The first
 // q_blocks workgroups: q in place, 32 (row, head) vectors per workgroup, 8
-// lanes each.  The rest: one workgroup per (segment, 32-key tile, KV head):
-// the tile's k rows normalised and rotated the same way (8 lanes per key),
-// staged in LDS and written to the K planes 16 bytes per slot (keys past the
-// segment as zeros), then the tile's V in four 32-dim passes.
+// lanes each.  The rest: one workgroup per (segment, 32-key tile, KV head,
+// quarter qd): keys 8qd..8qd+7 of the tile normalised and rotated the same way
+// (8 lanes per key), staged in LDS and written to the K planes 16 bytes per
+// slot (keys past the segment as zeros), and the tile's V dims 32qd..+31.
 __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
     float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ qw,
     const float* __restrict__ kw, int64_t rows, int n_heads, const float* __restrict__ cos_tab,
@@ -472,7 +472,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
     AttnSplit sp) {
   constexpr int D = kAttnD, half = D / 2;
   __shared__ float tile[32][33];
-  __shared__ float kt_s[32][D + 4];  // one key tile, normalised and rotated
+  __shared__ float kt_s[8][D + 4];  // 8 keys of a tile, normalised and rotated
   const int j = threadIdx.x & 7;
   if ((int64_t)blockIdx.x < q_blocks) {
     const int64_t task = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
@@ -487,19 +487,21 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
     for (int i = 0; i < 16; ++i) v[j + 8 * i] = x[i];
     return;
   }
-  // (segment, key tile, KV head)
+  // (segment, key tile, KV head, quarter)
   const int64_t job = (int64_t)blockIdx.x - q_blocks;
-  const int per_seg = ktiles * sp.n_kv_heads;
+  const int per_seg = ktiles * sp.n_kv_heads * 4;
   const int s = (int)(job / per_seg);
-  const int rem = (int)(job - (int64_t)s * per_seg);
-  const int ktile = rem / sp.n_kv_heads, kvh = rem - ktile * sp.n_kv_heads;
+  int rem = (int)(job - (int64_t)s * per_seg);
+  const int ktile = rem / (sp.n_kv_heads * 4);
+  rem -= ktile * sp.n_kv_heads * 4;
+  const int kvh = rem >> 2, qd = rem & 3;
   const AttnSeg seg = a.segs[s];
   const int t0 = ktile * 32;
   if (t0 >= seg.rows) return;  // uniform for the workgroup
   const int64_t r0 = seg.kv_off / a.kv_stride;  // the segment's first k row
   bool bad = false;
-  {
-    const int key = threadIdx.x >> 3;
+  if (threadIdx.x < 64) {
+    const int kq = threadIdx.x >> 3, key = 8 * qd + kq;
     float x[16];
     if (t0 + key < seg.rows) {
       const int64_t r = r0 + t0 + key;
@@ -512,19 +514,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
       for (int i = 0; i < 16; ++i) x[i] = 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) kt_s[key][j + 8 * i] = x[i];
+    for (int i = 0; i < 16; ++i) kt_s[kq][j + 8 * i] = x[i];
   }
   __syncthreads();
-  {
+  if (threadIdx.x < 128) {
     // slots: (key, 8-dim group g) -> fragment g/2, lane key + 32*(g%2)
     const int64_t nkb = sp.vt_cols / 32, kb = sp.vt_off[s] / 32 + ktile;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int slot = threadIdx.x + 256 * u, key = slot & 31, g = slot >> 5;
+    {
+      const int kq = threadIdx.x & 7, key = 8 * qd + kq, g = threadIdx.x >> 3;
       h8 hh, ll;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float xv = kt_s[key][8 * g + e];
+        const float xv = kt_s[kq][8 * g + e];
         bad |= !(fabsf(xv) < 65504.f);
         _Float16 hi, lo;
         split16(xv, hi, lo);
@@ -536,11 +537,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
       *reinterpret_cast<h8*>(sp.kl + ki) = ll;
     }
   }
-#pragma unroll 1
-  for (int dq = 0; dq < 4; ++dq) {
-    __syncthreads();  // `tile` is reused by each pass
-    bad |= split_v_tile(a, sp, s, ktile, kvh, dq, tile, false, false);
-  }
+  bad |= split_v_tile(a, sp, s, ktile, kvh, qd, tile, false, false);
   if (bad) atomicOr(sp.overflow, 1u);
 }
 
@@ -1255,7 +1252,7 @@ hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const 
     return hipErrorInvalidValue;
   const int64_t q_blocks = (rows * n_heads + 31) / 32;
   const int ktiles = (max_rows + 31) / 32;
-  const int64_t kv_jobs = args.n_segs > 0 ? (int64_t)args.n_segs * ktiles * n_kv_heads : 0;
+  const int64_t kv_jobs = args.n_segs > 0 ? (int64_t)args.n_segs * ktiles * n_kv_heads * 4 : 0;
   hipLaunchKernelGGL(qk_norm_rope_split_kernel, dim3((unsigned)(q_blocks + kv_jobs)), dim3(256), 0,
                      st, q, k, qw, kw, rows, n_heads, cos_tab, sin_tab, eps, q_blocks, ktiles,
                      args, sp);
