@@ -71,6 +71,7 @@ struct AttnSplit {
   // fp32 `out`; needs q_stride == out_stride and segment q offsets in whole rows.
   int8_t* aq;
   float* asc;
+  bool aq_tiled;  // codes tile-major (act_index), as the runner's GEMM reads them
 };
 // Splits K and V of the segments into the planes, then attends.
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,

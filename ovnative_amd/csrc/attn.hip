@@ -862,7 +862,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     }
     if (!valid) return;
     const int64_t col = (int64_t)h * kAttnD + d0;
-    *reinterpret_cast<i32x4*>(sp.aq + row * args.out_stride + col) = codes;
+    *reinterpret_cast<i32x4*>(sp.aq + act_index(row, col, args.out_stride, sp.aq_tiled)) = codes;
     if ((threadIdx.x & 1) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(amax, 127.0f);
     return;
   }
@@ -1152,7 +1152,8 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
         if (valid) {
           const int64_t row = seg.q_off / args.q_stride + q0 + i;
           const int64_t col = (int64_t)h * kAttnD + 4 * r32;
-          *reinterpret_cast<uint32_t*>(sp.aq + row * args.out_stride + col) = packed;
+          *reinterpret_cast<uint32_t*>(sp.aq + act_index(row, col, args.out_stride, sp.aq_tiled)) =
+              packed;
           if ((r32 & 7) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(a, 127.0f);
         }
       } else if (valid) {

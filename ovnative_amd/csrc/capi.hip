@@ -104,6 +104,54 @@ int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t 
 }
 }  // namespace ovh
 
+namespace ovh {
+int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
+             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled) {
+  if (M <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, asc, w);
+  if (rc != OV_OK) return rc;
+  if (!C) return fail(OV_ERR_INVALID_ARG, "C is null");
+  if (ldc < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldc < N");
+  ovh::GemmArgs a = base_args(M, aq, asc, w);
+  a.a_tiled = a_tiled;
+  a.nslices = 1;
+  a.start[0] = 0;
+  a.start[1] = (int)w->w.N;
+  a.out[0] = C;
+  a.ld[0] = ldc;
+  OVH_HIP(ovh::launch_gemm(a, accumulate ? ovh::kAccumulate : ovh::kStore, st), "gemm launch");
+  return OV_OK;
+}
+
+int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                    const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
+                    bool a_tiled) {
+  if (M <= 0 || n_slices <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, asc, w);
+  if (rc != OV_OK) return rc;
+  if (!slice_n || !slice_c) return fail(OV_ERR_INVALID_ARG, "slices are null");
+  if (n_slices > ovh::kMaxSlices)
+    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: at most 8 slices");
+  ovh::GemmArgs a = base_args(M, aq, asc, w);
+  a.a_tiled = a_tiled;
+  int64_t total = 0;
+  a.nslices = n_slices;
+  for (int s = 0; s < n_slices; ++s) {
+    if (slice_n[s] <= 0 || slice_n[s] % 64 != 0 || !slice_c[s])
+      return fail(OV_ERR_INVALID_ARG, "sliced GEMM: each slice N must be a positive multiple of 64");
+    a.start[s] = (int)total;
+    a.out[s] = slice_c[s];
+    a.ld[s] = slice_n[s];
+    total += slice_n[s];
+  }
+  if (total != w->w.N)
+    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: slice widths must sum to the weight's N");
+  a.start[n_slices] = (int)total;
+  OVH_HIP(ovh::launch_gemm(a, ovh::kStore, st), "gemm launch");
+  return OV_OK;
+}
+}  // namespace ovh
+
 extern "C" {
 
 const char* ovh_last_error(void) { return t_err.c_str(); }
@@ -277,47 +325,13 @@ int ovh_silu_mul_quantize(int64_t M, int64_t K, const float* gate, const float* 
 
 int ovh_linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
                  int64_t ldc, int accumulate, void* stream) {
-  if (M <= 0) return OV_OK;
-  int rc = check_gemm_operands(M, aq, asc, w);
-  if (rc != OV_OK) return rc;
-  if (!C) return fail(OV_ERR_INVALID_ARG, "C is null");
-  if (ldc < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldc < N");
-  ovh::GemmArgs a = base_args(M, aq, asc, w);
-  a.nslices = 1;
-  a.start[0] = 0;
-  a.start[1] = (int)w->w.N;
-  a.out[0] = C;
-  a.ld[0] = ldc;
-  OVH_HIP(ovh::launch_gemm(a, accumulate ? ovh::kAccumulate : ovh::kStore, as_stream(stream)),
-          "gemm launch");
-  return OV_OK;
+  return ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), false);
 }
 
 int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                         const int64_t* slice_n, float* const* slice_c, int n_slices,
                         void* stream) {
-  if (M <= 0 || n_slices <= 0) return OV_OK;
-  int rc = check_gemm_operands(M, aq, asc, w);
-  if (rc != OV_OK) return rc;
-  if (!slice_n || !slice_c) return fail(OV_ERR_INVALID_ARG, "slices are null");
-  if (n_slices > ovh::kMaxSlices)
-    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: at most 8 slices");
-  ovh::GemmArgs a = base_args(M, aq, asc, w);
-  int64_t total = 0;
-  a.nslices = n_slices;
-  for (int s = 0; s < n_slices; ++s) {
-    if (slice_n[s] <= 0 || slice_n[s] % 64 != 0 || !slice_c[s])
-      return fail(OV_ERR_INVALID_ARG, "sliced GEMM: each slice N must be a positive multiple of 64");
-    a.start[s] = (int)total;
-    a.out[s] = slice_c[s];
-    a.ld[s] = slice_n[s];
-    total += slice_n[s];
-  }
-  if (total != w->w.N)
-    return fail(OV_ERR_INVALID_ARG, "sliced GEMM: slice widths must sum to the weight's N");
-  a.start[n_slices] = (int)total;
-  OVH_HIP(ovh::launch_gemm(a, ovh::kStore, as_stream(stream)), "gemm launch");
-  return OV_OK;
+  return ovh::linear_q_sliced(M, aq, asc, w, slice_n, slice_c, n_slices, as_stream(stream), false);
 }
 
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,

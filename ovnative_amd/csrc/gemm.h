@@ -24,8 +24,11 @@ struct DeviceWeight {
 struct GemmArgs {
   int M = 0, N = 0, Kb = 0;
   int64_t Kp = 0;
-  const int8_t* aq = nullptr;   // [M][Kp]
+  const int8_t* aq = nullptr;   // [M][Kp], or tile-major (a_tiled)
   const float* asc = nullptr;   // [M][Kb]
+  // aq in the weight tile layout ([ceil(M/32)][Kb][64 lanes][16 B], rows past M
+  // zero): the A tiles then come in as 1 KiB contiguous DMA like the weights
+  int a_tiled = 0;
   const int8_t* W = nullptr;    // [Npad][Kp]
   const float* ws = nullptr;    // [Npad]
   int nslices = 1;
@@ -39,6 +42,7 @@ struct GemmArgs {
   int8_t* hq = nullptr;
   float* hsc = nullptr;
   int64_t hKp = 0;
+  int h_tiled = 0;  // hq tile-major (act_index)
 };
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);

@@ -363,6 +363,9 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     if (r < WT) {
       src[t] = a.W + ((int64_t)(n0 / 32 + r) * Kb + bb) * TILE + lane * 16;
       step[t] = (int64_t)SB * TILE;
+    } else if (a.a_tiled) {
+      src[t] = a.aq + ((int64_t)(m0 / 32 + r - WT) * Kb + bb) * TILE + lane * 16;
+      step[t] = (int64_t)SB * TILE;
     } else {
       int row = m0 + (r - WT) * 32 + (lane & 31);
       row = row < a.M ? row : a.M - 1;  // rows are independent: clamp, discard later
@@ -583,9 +586,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
         }
         if (m >= a.M) continue;
         const int64_t col = (int64_t)((n0 + (wn * FN + t) * 16) / 32) * 16;  // h column of the block
-        int8_t* dst = a.hq + (int64_t)m * a.hKp + col + 4 * q;
-        *reinterpret_cast<uint32_t*>(dst) = c0;
-        *reinterpret_cast<uint32_t*>(dst + 16) = c1;
+        *reinterpret_cast<uint32_t*>(a.hq + act_index(m, col + 4 * q, a.hKp, a.h_tiled)) = c0;
+        *reinterpret_cast<uint32_t*>(a.hq + act_index(m, col + 16 + 4 * q, a.hKp, a.h_tiled)) = c1;
         if (q == 0) a.hsc[(int64_t)m * (a.hKp / 32) + col / 32] = __fdiv_rn(am, 127.0f);
       }
     }

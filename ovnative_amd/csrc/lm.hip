@@ -34,6 +34,7 @@
 #include "attn.h"
 #include "ovh_common.h"
 #include "status.h"
+#include "quant.h"
 #include "weight.h"
 
 namespace ovh {
@@ -537,6 +538,12 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // Masks that are all ones add a zero bias: skip them.
   // The split attention takes masks as bit words, the fp32 kernel as biases.
   const bool split = L.attn_split && (int)segs.size() <= ovh::kAttnMaxSegs;
+  // Activation codes tile-major on the main path (split attention, SiLU in the
+  // gate/up epilogue, a hidden width the RMSNorm rows kernel takes): every
+  // GEMM then moves its A tiles as 1 KiB contiguous DMA.  Rows are padded to a
+  // multiple of 128 (the tallest GEMM tile reads whole tiles).
+  const bool tiled = split && L.silu_fused && H % 256 == 0 && H <= 1024;
+  const int64_t Tpad = (T + 127) / 128 * 128;
   std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
   int64_t bias_elems = 0, bits_words = 0;
   for (size_t i = 0; i < segs.size(); ++i) {
@@ -568,10 +575,11 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
             b_bias = take(split ? 0 : sizeof(float) * (size_t)bias_elems),
             b_bits = take(split ? sizeof(uint32_t) * (size_t)bits_words : 0),
             b_x = take(sizeof(float) * (size_t)(T * H)),
-            b_aq = take((size_t)(T * Kp_max)), b_asc = take(sizeof(float) * (size_t)(T * Kb_max)),
+            b_aq = take((size_t)(Tpad * Kp_max)), b_asc = take(sizeof(float) * (size_t)(T * Kb_max)),
             b_q = take(sizeof(float) * (size_t)(T * QD)), b_k = take(sizeof(float) * (size_t)(T * KVD)),
             b_v = take(sizeof(float) * (size_t)(T * KVD)), b_at = take(sizeof(float) * (size_t)(T * QD)),
-            b_g = take(sizeof(float) * (size_t)(T * I)), b_u = take(sizeof(float) * (size_t)(T * I)),
+            b_g = take(sizeof(float) * (size_t)(Tpad * I)),  // also the SiLU codes, Tpad rows
+            b_u = take(sizeof(float) * (size_t)(T * I)),
             b_lg = take(sizeof(float) * (size_t)(T * CV));
   // split-f16 attention planes (K and V tile-major, segments padded to 32 keys)
   int64_t vt_cols = 0;
@@ -668,6 +676,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     sp.overflow = L.d_overflow;
     sp.aq = aq;  // attention writes the o_proj input already quantised
     sp.asc = asc;
+    sp.aq_tiled = tiled;
   }
   // The inputs go up first, in one copy; the staging buffer may be refilled
   // once it is done.
@@ -677,6 +686,12 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // embedding, the layers, final norm and head.
   auto enqueue = [&]() -> int {
     int rc = OV_OK;
+    auto norm_q = [&](const float* w) -> int {
+      if (!tiled) return ovh_rmsnorm_quantize(T, H, x, w, c.rms_eps, aq, asc, st);
+      OVH_HIP(ovh::launch_rmsnorm_quantize(T, H, x, w, c.rms_eps, aq, asc, st, true),
+              "rmsnorm launch");
+      return OV_OK;
+    };
     for (size_t i = 0; i < segs.size(); ++i) {
       if (bias_off[i] < 0) continue;
       const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
@@ -698,8 +713,9 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     const int64_t gu_n[2] = {I, I};
     float* gu_c[2] = {gate, up};
     for (const OvhLm::Layer& Y : L.layers) {
-      if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln1, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
-      if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st)) != OV_OK) return rc;
+      if ((rc = norm_q(Y.ln1)) != OV_OK) return rc;
+      if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled)) != OV_OK)
+        return rc;
       if (split) {
         // q/k norm + RoPE, f16 planes of k and V, then attention
         OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
@@ -715,8 +731,8 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           return rc;
       }
       if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
-      if ((rc = ovh_linear_q(T, aq, asc, Y.o, x, H, 1, st)) != OV_OK) return rc;
-      if ((rc = ovh_rmsnorm_quantize(T, H, x, Y.ln2, c.rms_eps, aq, asc, st)) != OV_OK) return rc;
+      if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled)) != OV_OK) return rc;
+      if ((rc = norm_q(Y.ln2)) != OV_OK) return rc;
       if (L.silu_fused) {
         // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
         // (otherwise unused) gate/up buffers: codes [T][I], scales [T][I/32]
@@ -732,17 +748,19 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         ga.hq = reinterpret_cast<int8_t*>(gate);
         ga.hsc = up;
         ga.hKp = I;
+        ga.a_tiled = tiled;
+        ga.h_tiled = tiled;
         OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
-        if ((rc = ovh_linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st)) != OV_OK) return rc;
+        if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled)) != OV_OK) return rc;
       } else {
         if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
         if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
         if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
       }
     }
-    if ((rc = ovh_rmsnorm_quantize(T, H, x, L.final_norm, c.rms_eps, aq, asc, st)) != OV_OK)
+    if ((rc = norm_q(L.final_norm)) != OV_OK)
       return rc;
-    return ovh_linear_q(T, aq, asc, L.head, logits, CV, 0, st);
+    return ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled);
   };
 
   if (!L.use_graphs) {

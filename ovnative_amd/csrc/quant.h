@@ -8,8 +8,11 @@ namespace ovh {
 
 hipError_t launch_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
                            hipStream_t st);
+// tiled: codes tile-major (act_index); needs cols % 256 == 0, cols <= 1024 and
+// 16-byte aligned x and w (hipErrorInvalidValue otherwise).
 hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
-                                   float eps, int8_t* aq, float* asc, hipStream_t st);
+                                   float eps, int8_t* aq, float* asc, hipStream_t st,
+                                   bool tiled = false);
 size_t rmsnorm_quantize_smem(int64_t cols);
 hipError_t launch_silu_mul_quantize(int64_t M, int64_t K, const float* g, const float* u,
                                     int8_t* aq, float* asc, hipStream_t st);

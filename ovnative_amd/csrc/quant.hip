@@ -167,7 +167,8 @@ __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* 
                                                                    const float* __restrict__ w,
                                                                    float eps,
                                                                    int8_t* __restrict__ aq,
-                                                                   float* __restrict__ asc) {
+                                                                   float* __restrict__ asc,
+                                                                   bool tiled) {
   constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
   __shared__ __attribute__((aligned(16))) float xt[8 * TP];
   const int lane = threadIdx.x;
@@ -202,7 +203,6 @@ __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* 
   for (int j = 1; j < 8; ++j) sum = __fadd_rn(sum, __shfl(part, j));
   const float scale =
       __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
-  int8_t* qrow = aq + r * cols;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     float v[4];
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* 
     for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(xv[p][i], scale), wv[p][i]);
     uint32_t codes;
     const float s = quant_block_lane(v, 4, &codes);
-    *reinterpret_cast<uint32_t*>(qrow + 256 * p + 4 * lane) = codes;
+    *reinterpret_cast<uint32_t*>(aq + act_index(r, 256 * p + 4 * lane, cols, tiled)) = codes;
     if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
   }
 }
@@ -293,12 +293,12 @@ size_t rmsnorm_quantize_smem(int64_t cols) {
 }
 
 hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, const float* w,
-                                   float eps, int8_t* aq, float* asc, hipStream_t st) {
+                                   float eps, int8_t* aq, float* asc, hipStream_t st, bool tiled) {
   const int64_t Kb = kb_of(cols);
   if (cols % 256 == 0 && cols <= 1024 && aligned16(x) && aligned16(w)) {
     const dim3 grid((unsigned)rows), block(64);
     auto go = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, grid, block, 0, st, x, w, eps, aq, asc);
+      hipLaunchKernelGGL(kernel, grid, block, 0, st, x, w, eps, aq, asc, tiled);
     };
     switch (cols / 256) {
       case 1: go(rmsnorm_quantize_rows_kernel<1>); break;
@@ -308,6 +308,7 @@ hipError_t launch_rmsnorm_quantize(int64_t rows, int64_t cols, const float* x, c
     }
     return hipGetLastError();
   }
+  if (tiled) return hipErrorInvalidValue;
   const int rpb = rms_rows_per_block(rows);
   const size_t smem = sizeof(float) * (size_t)rpb * (size_t)(cols + 8);
   const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(64 * rpb);

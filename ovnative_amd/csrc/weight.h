@@ -16,4 +16,11 @@ namespace ovh {
 // (scales alike): the operand of the SiLU-fused GEMM mode.
 int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
                         OvhWeight** out);
+// ovh_linear_q / ovh_linear_q_sliced, with the codes aq tile-major
+// (act_index; rows up to a multiple of 128 readable) when a_tiled.
+int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
+             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled);
+int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                    const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
+                    bool a_tiled);
 }  // namespace ovh

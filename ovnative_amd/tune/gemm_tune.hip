@@ -59,3 +59,20 @@ extern "C" int tune_gemm_silu(int pipe, int M, int N, int Kb, const int8_t* aq, 
   return pipe ? launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, s)
               : launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, s);
 }
+
+// tune_gemm with the activation codes tile-major (GemmArgs::a_tiled).
+extern "C" int tune_gemm_at(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
+                            const int8_t* W, const float* ws, float* C, int accumulate, void* st,
+                            int a_tiled) {
+  GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
+  a.W = W; a.ws = ws; a.nslices = 1; a.start[0] = 0; a.start[1] = N; a.out[0] = C; a.ld[0] = N;
+  a.a_tiled = a_tiled;
+  GemmMode mode = accumulate ? kAccumulate : kStore;
+  hipStream_t s = (hipStream_t)st;
+  switch (cfg) {
+    case 8: return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, s);
+    case 9: return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, s);
+    case 32: return launch_cfg16<128, 64, 4, 2, 4, 2, false>(a, mode, s);
+  }
+  return -1;
+}
