@@ -896,12 +896,13 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // are stored (1 KiB each, lane-linear), so the DMA copies them verbatim and a
 // wavefront's fragment read is 64 contiguous 16-byte slots (conflict-free).
 constexpr int kLdsPlane = 32 * kAttnD;  // halves per plane per block
-// The long-sequence form pays once segments are long and its workgroups fill
-// the chip (MI355X: 16 x 1024 rows 41.6 vs 42.7 ms per LM forward with the
-// form above); with few segments the form above has 4x the workgroups and
-// wins (2 x 1024 rows: 74 vs 82 us).
-constexpr int kLdsMinRows = 640;
-constexpr int kLdsMinTasks = 512;
+// The long-sequence form pays once its workgroups (segments x KV heads x
+// 128-row tiles) fill the chip about one and a half times over; below that
+// the form above, with 4x the workgroups, is faster.  MI355X, 16/8 heads,
+// us (short form / this form, tasks of this form): 2 x 300 15.1 / 22.9 (80),
+// 8 x 300 39.5 / 41.7 (320), 4 x 768 87.6 / 80.4 (384), 2 x 1024 76.3 / 73.3
+// (256), 8 x 512 86.0 / 65.7 (512), 16 x 300 73.7 / 63.0 (640).
+constexpr int kLdsMinTasks = 384;
 
 template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs args, AttnSplit sp,
@@ -1191,9 +1192,9 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   const int QT = kAttnWaves * kAttnQ / args.group;  // query rows per long-form workgroup
   const int lds_qtiles = (max_rows + QT - 1) / QT;
   const int lds_tasks = args.n_segs * (args.n_heads / args.group) * lds_qtiles;
-  if (max_rows >= kLdsMinRows && lds_tasks >= kLdsMinTasks && kAttnWaves % args.group == 0) {
-    // long segments, many of them: K/V blocks shared through LDS by 128
-    // query-head rows
+  if (lds_tasks >= kLdsMinTasks && kAttnWaves % args.group == 0) {
+    // a chip's worth of long-form workgroups: K/V blocks shared through LDS
+    // by 128 query-head rows
     const int qtiles = lds_qtiles;
     const int tasks = lds_tasks;
     const int per_xcd = (tasks + 7) / 8;
