@@ -3,10 +3,12 @@
 // of libovnative_amd.so.
 #include "../csrc/gemm.hip"
 using namespace ovh;
-extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
-                         const int8_t* W, const float* ws, float* C, int accumulate, void* st) {
+static int run_cfg(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
+                   const int8_t* W, const float* ws, float* C, int accumulate, void* st,
+                   int a_tiled) {
   GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
   a.W = W; a.ws = ws; a.nslices = 1; a.start[0] = 0; a.start[1] = N; a.out[0] = C; a.ld[0] = N;
+  a.a_tiled = a_tiled;
   GemmMode mode = accumulate ? kAccumulate : kStore;
   hipStream_t s = (hipStream_t)st;
   switch (cfg) {
@@ -60,19 +62,15 @@ extern "C" int tune_gemm_silu(int pipe, int M, int N, int Kb, const int8_t* aq, 
               : launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, s);
 }
 
-// tune_gemm with the activation codes tile-major (GemmArgs::a_tiled).
+extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
+                         const int8_t* W, const float* ws, float* C, int accumulate, void* st) {
+  return run_cfg(cfg, M, N, Kb, aq, asc, W, ws, C, accumulate, st, 0);
+}
+// tune_gemm with the activation codes tile-major (GemmArgs::a_tiled; the 16x16
+// configs only).
 extern "C" int tune_gemm_at(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
                             const int8_t* W, const float* ws, float* C, int accumulate, void* st,
                             int a_tiled) {
-  GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
-  a.W = W; a.ws = ws; a.nslices = 1; a.start[0] = 0; a.start[1] = N; a.out[0] = C; a.ld[0] = N;
-  a.a_tiled = a_tiled;
-  GemmMode mode = accumulate ? kAccumulate : kStore;
-  hipStream_t s = (hipStream_t)st;
-  switch (cfg) {
-    case 8: return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, s);
-    case 9: return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, s);
-    case 32: return launch_cfg16<128, 64, 4, 2, 4, 2, false>(a, mode, s);
-  }
-  return -1;
+  if (a_tiled && cfg < 8) return -1;
+  return run_cfg(cfg, M, N, Kb, aq, asc, W, ws, C, accumulate, st, a_tiled);
 }
