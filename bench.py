@@ -80,9 +80,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", choices=("step", "m16384"), default="step",
+    p.add_argument("--workload", choices=("step", "m16384", "linear", "layer"), default="step",
                    help="step: BASELINE config 4 (the metric); m16384: config 5, one forward "
-                        "of 8 requests x CFG 2 x seq 1024 (M = 16384)")
+                        "of 8 requests x CFG 2 x seq 1024 (M = 16384); linear: config 1, one "
+                        "quantise + int8 linear at M=256, K=1024, N=3072; layer: config 3, one "
+                        "decoder layer at M=2x300")
     return p.parse_args()
 
 
@@ -308,6 +310,228 @@ def cpu_baseline(cfg: dict, tensors, budget_s: float, batch=None):
     }
 
 
+def bench_line(args, value, unit, ms, config, roofline, cpu, wall, dtype="int8"):
+    return {
+        "metric": "int8 linear TOPS & % roofline; LM ms/step (seq 300, CFG batch 2)",
+        "value": value,
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": config,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_s": wall,
+    }
+
+
+def linear_inputs(M=256, K=1024, N=3072, seed=1234):
+    """A fp32 [M, K] ~N(0, 1) with 8 outlier channels x20, W
+    fp32 [N, K] ~N(0, 0.02) quantised per output channel as
+    tools/convert_weights.py:130-135 does (float32 scale = max(absmax/127,
+    1e-12), q = clip(rint(w / scale), -127, 127))."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    A[:, rng.choice(K, 8, replace=False)] *= np.float32(20.0)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    s = np.maximum(np.abs(W).max(axis=1) / np.float32(127.0), np.float32(1e-12)).astype(np.float32)
+    q = np.clip(np.rint(W / s[:, None]), -127, 127).astype(np.int8)
+    return A, q, s
+
+
+def run_linear(args) -> None:
+    """s8_nk_quantize of A then linear_s8_nk_packed_q, through
+    the C ABI (ovh_s8_nk_quantize + ovh_linear_q) on device-resident inputs.  One
+    step = the pair of launches; the GEMM alone is timed too for its roofline
+    (HBM-bound: 6.60 MB of algorithmic traffic against 1.61 GOP)."""
+    import numpy as np
+    import torch
+    import ovnative_amd as ov
+    M, K, N = 256, 1024, 3072
+    A, q, s = linear_inputs(M, K, N)
+    w = ov.Weight.from_host(q, s)
+    lib = ov.load()
+    st = torch.cuda.current_stream().cuda_stream
+    dA = torch.from_numpy(A).cuda()
+    Kb = (K + 31) // 32
+    aq = torch.empty((M, 32 * Kb), dtype=torch.int8, device="cuda")
+    asc = torch.empty((M, Kb), dtype=torch.float32, device="cuda")
+    C_ = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    qargs = (M, K, dA.data_ptr(), aq.data_ptr(), asc.data_ptr(), st)
+    largs = (M, aq.data_ptr(), asc.data_ptr(), w.handle, C_.data_ptr(), N, 0, st)
+
+    def timed(fns, reps):
+        for _ in range(args.warmup):
+            for f, a in fns:
+                if f(*a) != 0:
+                    raise RuntimeError("C ABI call failed")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for f, a in fns:
+                f(*a)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    t0 = time.perf_counter()
+    reps = max(args.steps, 200)
+    ms_pair = timed([(lib.ovh_s8_nk_quantize, qargs), (lib.ovh_linear_q, largs)], reps)
+    ms_gemm = timed([(lib.ovh_linear_q, largs)], reps)
+    ms_quant = timed([(lib.ovh_s8_nk_quantize, qargs)], reps)
+    wall = time.perf_counter() - t0
+    ops = 2 * M * N * K
+    gemm_bytes = N * K + 4 * N + M * 32 * Kb + 4 * M * Kb + 4 * M * N
+    log(f"config 1: quantise + linear {ms_pair * 1e3:.2f} us (quantise {ms_quant * 1e3:.2f}, "
+        f"linear {ms_gemm * 1e3:.2f}); linear {gemm_bytes / ms_gemm / 1e6:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        impl, kind = None, None
+        if oracle.reference_available():
+            try:
+                r = oracle.Reference()
+                if r.vnni_available():
+                    impl, kind = r, "reference"
+            except OSError:
+                impl = None
+        if impl is None:
+            o = oracle.Oracle()
+            if o.fast_available():
+                impl, kind = o, "port"
+        if impl is not None:
+            packed, wsum = impl.pack(q)
+            Cc = np.zeros((M, N), np.float32)
+            times = []
+            t_end = time.perf_counter() + min(args.cpu_seconds, 10.0)
+            while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 500):
+                t1 = time.perf_counter()
+                caq, casc = impl.quantize(A)
+                impl.linear_q_packed(caq, casc, packed, wsum, N, K, s, Cc)
+                times.append(time.perf_counter() - t1)
+            sec = statistics.median(times)
+            cpu = {"value": round(ops / sec / 1e12, 4), "unit": "TOPS",
+                   "cores": oracle.Oracle().num_threads(), "kind": kind,
+                   "sample": (f"s8_nk_quantize + linear_s8_nk_packed_q at M={M}, K={K}, N={N} "
+                              f"({'reference gemm.cpp' if kind == 'reference' else 'oracle restatement'}"
+                              f"), median of {len(times)}"),
+                   "ms_per_step": round(sec * 1e3, 4)}
+    frac_gb = gemm_bytes / ms_gemm / 1e6
+    line = bench_line(
+        args, round(ops / (ms_pair * 1e-3) / 1e12, 2), "TOPS", round(ms_pair, 5),
+        {"workload": (f"BASELINE config 1: s8_nk_quantize of A fp32 [{M},{K}] (~N(0,1), 8 outlier "
+                      f"channels x20) + int8-nk linear to C fp32 [{M},{N}] (W ~N(0,0.02), per-channel "
+                      "int8), inputs resident in HBM"),
+         "model": "single linear (MLP up-proj shape)", "global_batch": M, "seq_len": 1,
+         "parallelism": "single GPU", "quantize_ms": round(ms_quant, 5),
+         "linear_ms": round(ms_gemm, 5)},
+        {"bound": "hbm", "kernel": f"gemm16 store (M={M}, N={N}, K={K})",
+         "achieved": round(frac_gb, 1), "peak": 8000.0, "unit": "GB/s",
+         "frac": round(frac_gb / 8000.0, 4), "traffic": None, "avg_ms": round(ms_gemm, 5),
+         "algorithmic_bytes": gemm_bytes},
+        cpu, round(wall, 3))
+    w.free()
+    print(json.dumps(line), flush=True)
+
+
+def run_layer(args) -> None:
+    """one decoder layer at M = 2 x 300 (the config-4 CFG batch),
+    measured as the difference of the runner's forward at 2 layers and at 1 layer
+    (same embedding, final norm and head on both sides), with the reference's
+    LM::forward timed the same way on the host."""
+    import torch
+    import ovnative_amd as ov
+    cfg2 = dict(CFG, n_layers=2)
+    cfg1 = dict(CFG, n_layers=1)
+    t_setup = time.perf_counter()
+    tensors = make_checkpoint(cfg2)
+    ids, am, attn, pos, _ = make_inputs(cfg2)
+    log(f"checkpoint {time.perf_counter() - t_setup:.1f}s")
+    t0 = time.perf_counter()
+    ms = {}
+    for n, cfg in ((1, cfg1), (2, cfg2)):
+        lm = ov.LM.from_tensors(tensors, ov.LmConfig(**cfg))
+        for _ in range(max(args.warmup, 3)):
+            lm.forward(ids, am, attn, pos, host_logits=False)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(args.steps, 50)
+        e0.record()
+        for _ in range(reps):
+            lm.forward(ids, am, attn, pos, host_logits=False)
+        e1.record()
+        torch.cuda.synchronize()
+        ms[n] = e0.elapsed_time(e1) / reps
+        lm.close()
+    wall = time.perf_counter() - t0
+    M = SEQ * CFG_BATCH
+    layer_ms = ms[2] - ms[1]
+    layer_ops = linear_ops(cfg1, M, 1) - linear_ops(cfg1, M, 0)
+    tops = layer_ops / (layer_ms * 1e-3) / 1e12
+    log(f"config 3: forward 1 layer {ms[1]:.3f} ms, 2 layers {ms[2]:.3f} ms -> layer "
+        f"{layer_ms * 1e3:.1f} us ({tops:.1f} linear TOPS)")
+    rs_ms, rs_ops = time_residual(CFG, 1, M, reps=16)
+    rs_tops = rs_ops / (rs_ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        if oracle.reference_available():
+            try:
+                ref = oracle.Reference()
+                ref = ref if ref.vnni_available() else None
+            except OSError:
+                ref = None
+            if ref is not None:
+                from ovnative_amd import ovw1
+                sec = {}
+                with tempfile.TemporaryDirectory() as d:
+                    path = os.path.join(d, "lm.ovw")
+                    ovw1.write(path, tensors)
+                    for n, cfg in ((1, cfg1), (2, cfg2)):
+                        h = ref.lm_open(path, cfg)
+                        try:
+                            ref.lm_forward(h, cfg, ids, am, attn, pos)
+                            times = []
+                            t_end = time.perf_counter() + args.cpu_seconds / 2
+                            while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
+                                t1 = time.perf_counter()
+                                ref.lm_forward(h, cfg, ids, am, attn, pos)
+                                times.append(time.perf_counter() - t1)
+                        finally:
+                            ref.lm_close(h)
+                        sec[n] = (statistics.median(times), len(times))
+                layer_s = sec[2][0] - sec[1][0]
+                cpu = {"value": round(layer_ops / layer_s / 1e12, 4), "unit": "TOPS",
+                       "cores": oracle.Oracle().num_threads(), "kind": "reference",
+                       "sample": (f"reference LM::forward at 2 layers (median of {sec[2][1]}) minus "
+                                  f"1 layer (median of {sec[1][1]}), B=2, S={SEQ}"),
+                       "ms_per_step": round(layer_s * 1e3, 3)}
+    line = bench_line(
+        args, round(tops, 2), "TOPS", round(layer_ms, 5),
+        {"workload": (f"BASELINE config 3: one Qwen3-0.6B-shaped decoder layer at M=2x{SEQ} (the "
+                      "config-4 CFG batch): RMSNorm+quant, merged q/k/v, qk-norm+RoPE, GQA "
+                      "attention (split-f16), o_proj (+= x), RMSNorm+quant, gate/up+SiLU, down "
+                      "(+= x); runner forward at 2 layers minus 1 layer"),
+         "model": "one decoder layer (hidden 1024, 16/8 heads x 128, inter 3072)",
+         "global_batch": CFG_BATCH, "seq_len": SEQ, "parallelism": "single GPU",
+         "layer_linear_gop": round(layer_ops / 1e9, 3),
+         "forward_1_layer_ms": round(ms[1], 4), "forward_2_layers_ms": round(ms[2], 4)},
+        {"bound": "mfma",
+         "kernel": f"gemm16 residual (o_proj K=2048 and down K=3072; M={M}, N=1024, += x; weights hot)",
+         "achieved": round(rs_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+         "frac": round(rs_tops / PEAK_INT8_TOPS, 4), "traffic": None, "avg_ms": round(rs_ms, 5)},
+        cpu, round(wall, 3))
+    print(json.dumps(line), flush=True)
+
+
 def run_m16384(args, cfg: dict, tensors) -> None:
     """8 concurrent requests x CFG 2 x seq 1024 (M = 16384)
     through the 28-layer LM; one step = one forward (logits left on the device)."""
@@ -392,6 +616,12 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.workload == "linear":
+        run_linear(args)
+        return
+    if args.workload == "layer":
+        run_layer(args)
+        return
     cfg = dict(CFG, n_layers=args.layers)
     M = SEQ * CFG_BATCH
     t_setup = time.perf_counter()

@@ -80,8 +80,6 @@ hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int
 // segments' masks from AttnSeg::bits when mask_bits, else from AttnSeg::bias.
 hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                        bool mask_bits, hipStream_t st);
-// uint8 mask [rows, rows] (non-zero = visible) -> AttnSeg::bits words.
-hipError_t launch_mask_bits(const uint8_t* mask, int rows, uint32_t* bits, hipStream_t st);
 // launch_qk_norm_rope (D = 128) that also writes the planes of the roped k rows
 // of args' segments (args.kv_stride = n_kv_heads * 128) and of their V, in one
 // launch.

@@ -1221,29 +1221,6 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   return hipGetLastError();
 }
 
-// One thread per 32-key word of a mask row.
-__global__ __launch_bounds__(256) void mask_bits_kernel(const uint8_t* __restrict__ mask, int rows,
-                                                        uint32_t* __restrict__ bits) {
-  const int words = (rows + 31) >> 5;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)rows * words) return;
-  const int64_t r = i / words;
-  const int w = (int)(i - r * words);
-  const uint8_t* src = mask + r * rows + 32 * w;
-  const int n = min(32, rows - 32 * w);
-  uint32_t b = 0;
-  for (int j = 0; j < n; ++j) b |= (src[j] != 0 ? 1u : 0u) << j;
-  bits[i] = b;
-}
-
-hipError_t launch_mask_bits(const uint8_t* mask, int rows, uint32_t* bits, hipStream_t st) {
-  const int64_t n = (int64_t)rows * ((rows + 31) / 32);
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(mask_bits_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, mask,
-                     rows, bits);
-  return hipGetLastError();
-}
-
 hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const float* kw,
                                      int64_t rows, int n_heads, int n_kv_heads,
                                      const float* cos_tab, const float* sin_tab, float eps,

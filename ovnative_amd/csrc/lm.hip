@@ -56,16 +56,88 @@ __device__ __forceinline__ float emb_at(const EmbTable& t, int64_t id, int64_t H
   return t.f32 ? t.f32[id * H + h] : __fmul_rn((float)t.i8[id * H + h], t.scale[id]);
 }
 
+// Columns h..h+3 of table row id (H % 4 == 0): one 4- or 16-byte load; zeros
+// for an id outside the table.
+__device__ __forceinline__ f32x4 emb4(const EmbTable& t, int64_t id, int64_t H, int64_t h) {
+  if (id < 0 || id >= t.rows) return f32x4{0.f, 0.f, 0.f, 0.f};
+  if (t.f32) return *reinterpret_cast<const f32x4*>(t.f32 + id * H + h);
+  const uint32_t q = *reinterpret_cast<const uint32_t*>(t.i8 + id * H + h);
+  const float sc = t.scale[id];
+  f32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r[k] = __fmul_rn((float)(int8_t)(q >> (8 * k)), sc);
+  return r;
+}
+
+// The attention masks of the forward's segments as AttnSeg::bits words (bit
+// t % 32 of word [row * ((rows + 31) / 32) + t / 32] set = key t visible),
+// done by extra workgroups of the embedding launch: four rows per workgroup,
+// one wavefront per row, 64 keys per ballot.
+struct MaskJob {
+  const uint8_t* mask;  // [rows, rows], non-zero = visible
+  uint32_t* bits;
+  int32_t rows;
+  int32_t first;  // first workgroup of this job, counted from the mask part
+};
+struct MaskJobs {
+  int32_t n;
+  MaskJob job[kAttnMaxSegs];
+};
+constexpr int kEmbMaxC = 16;  // codebooks the vector path holds in registers
+
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
                                                     const uint8_t* __restrict__ mask, int seq,
                                                     int C, int64_t H, EmbTable tok, EmbTable aud,
                                                     const int64_t* __restrict__ offsets,
-                                                    float* __restrict__ out) {
-  const int64_t row = blockIdx.x;
+                                                    float* __restrict__ out, int64_t T,
+                                                    MaskJobs mj) {
+  const int64_t wg = blockIdx.x;
+  if (wg >= T) {
+    const int64_t mw = wg - T;
+    int j = 0;
+    while (j + 1 < mj.n && mw >= mj.job[j + 1].first) ++j;
+    const MaskJob jb = mj.job[j];
+    const int r = (int)(mw - jb.first) * 4 + (int)(threadIdx.x >> 6);
+    if (r >= jb.rows) return;
+    const int lane = threadIdx.x & 63, words = (jb.rows + 31) >> 5;
+    const uint8_t* src = jb.mask + (int64_t)r * jb.rows;
+    for (int t0 = 0; t0 < jb.rows; t0 += 64) {
+      const int t = t0 + lane;
+      const uint64_t vis = __ballot(t < jb.rows && src[t < jb.rows ? t : 0] != 0);
+      const int w = (t0 >> 5) + lane;  // lanes 0 and 1 write the two words
+      if (lane < 2 && w < words) jb.bits[(int64_t)r * words + w] = (uint32_t)(vis >> (32 * lane));
+    }
+    return;
+  }
+  const int64_t row = wg;
   const int64_t b = row / seq, s = row - b * seq;
   float* o = out + row * H;
   // The host has range-checked every id; an id outside its table (which that
   // check rules out) reads nothing and contributes zeros.
+  if ((H & 3) == 0 && C <= kEmbMaxC) {
+    if (mask[row]) {
+      for (int64_t h = 4 * (int64_t)threadIdx.x; h < H; h += 4 * (int64_t)blockDim.x) {
+        // every codebook's values are loaded before the sum, which runs from 0
+        // in codebook order as above
+        f32x4 e[kEmbMaxC];
+#pragma unroll
+        for (int c = 0; c < kEmbMaxC; ++c)
+          if (c < C) e[c] = emb4(aud, ids[(b * C + c) * seq + s] + offsets[c], H, h);
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < kEmbMaxC; ++c)
+          if (c < C)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = __fadd_rn(acc[k], e[c][k]);
+        *reinterpret_cast<f32x4*>(o + h) = acc;
+      }
+    } else {
+      const int64_t id = ids[b * C * seq + s];
+      for (int64_t h = 4 * (int64_t)threadIdx.x; h < H; h += 4 * (int64_t)blockDim.x)
+        *reinterpret_cast<f32x4*>(o + h) = emb4(tok, id, H, h);
+    }
+    return;
+  }
   if (mask[row]) {
     for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
       float acc = 0.f;
@@ -692,21 +764,25 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
               "rmsnorm launch");
       return OV_OK;
     };
+    // masks: bit words (split form, built by the embedding launch) or fp32 bias
+    ovh::MaskJobs mj{};
+    int64_t mask_wgs = 0;
     for (size_t i = 0; i < segs.size(); ++i) {
       if (bias_off[i] < 0) continue;
-      const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
       const uint8_t* m = d_mask + bias_off[i];
       if (split) {
-        OVH_HIP(ovh::launch_mask_bits(m, segs[i].rows, const_cast<uint32_t*>(seg_bits[i]), st),
-                "mask_bits launch");
+        mj.job[mj.n++] = ovh::MaskJob{m, const_cast<uint32_t*>(seg_bits[i]), segs[i].rows,
+                                      (int32_t)mask_wgs};
+        mask_wgs += (segs[i].rows + 3) / 4;
       } else {
+        const int64_t n = (int64_t)segs[i].rows * segs[i].rows;
         hipLaunchKernelGGL(ovh::mask_to_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
                            0, st, m, const_cast<float*>(asegs[i].bias), n);
         OVH_HIP(hipGetLastError(), "mask_to_bias launch");
       }
     }
-    hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)T), dim3(256), 0, st, d_ids, d_am, seq,
-                       (int)C, H, L.tok, L.aud, L.d_offsets, x);
+    hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)(T + mask_wgs)), dim3(256), 0, st, d_ids,
+                       d_am, seq, (int)C, H, L.tok, L.aud, L.d_offsets, x, T, mj);
     OVH_HIP(hipGetLastError(), "embed launch");
     const int64_t qkv_n[3] = {QD, KVD, KVD};
     float* qkv_c[3] = {q, k, v};
