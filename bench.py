@@ -59,11 +59,11 @@ def attention_flops(cfg: dict, seq: int, batch: int, layers: int) -> int:
     return layers * batch * cfg["n_heads"] * 4 * seq * seq * cfg["head_dim"]
 
 
-def residual_traffic():
+def residual_traffic(name="gemm_residual_m600_traffic.json"):
     """HBM bytes per launch of the residual GEMM (mean of the o_proj and down
-    launches), from the committed PMC summary (FETCH_SIZE + WRITE_SIZE, scaled
-    by the copy-kernel calibration)."""
-    path = os.path.join(ROOT, "profiles", "gemm_residual_m600_traffic.json")
+    launches), or of the kernel another committed PMC summary names (FETCH_SIZE
+    + WRITE_SIZE, scaled by the copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             return json.load(f)["hbm_bytes_per_launch"]
@@ -80,11 +80,13 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="wall-clock budget of the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--workload", choices=("step", "m16384", "linear", "layer"), default="step",
+    p.add_argument("--workload", choices=("step", "m16384", "linear", "skinny", "layer"),
+                   default="step",
                    help="step: BASELINE config 4 (the metric); m16384: config 5, one forward "
                         "of 8 requests x CFG 2 x seq 1024 (M = 16384); linear: config 1, one "
-                        "quantise + int8 linear at M=256, K=1024, N=3072; layer: config 3, one "
-                        "decoder layer at M=2x300")
+                        "quantise + int8 linear at M=256, K=1024, N=3072; skinny: config 2, a "
+                        "layer's seven projections at M=2x64, weights cold; layer: config 3, "
+                        "one decoder layer at M=2x300")
     return p.parse_args()
 
 
@@ -435,10 +437,151 @@ def run_linear(args) -> None:
          "linear_ms": round(ms_gemm, 5)},
         {"bound": "hbm", "kernel": f"gemm16 store (M={M}, N={N}, K={K})",
          "achieved": round(frac_gb, 1), "peak": 8000.0, "unit": "GB/s",
-         "frac": round(frac_gb / 8000.0, 4), "traffic": None, "avg_ms": round(ms_gemm, 5),
+         "frac": round(frac_gb / 8000.0, 4),
+         "traffic": residual_traffic("gemm_linear_m256_traffic.json"), "avg_ms": round(ms_gemm, 5),
          "algorithmic_bytes": gemm_bytes},
         cpu, round(wall, 3))
     w.free()
+    print(json.dumps(line), flush=True)
+
+
+def run_skinny(args) -> None:
+    """the seven projections of a layer at M = 2 x 64 through
+    ovh_linear_q, weights cold (28 layers of distinct weights, 440 MB, rotated
+    so every launch streams its weight from HBM), plus the merged q/k/v and
+    gate/up weights the runner launches (ovh_linear_q_sliced).  value = weight
+    bytes (int8 + fp32 scales) of the seven projections / their summed time."""
+    import numpy as np
+    import torch
+    import ovnative_amd as ov
+    M, L = 128, 28
+    H, QD, KVD, I = CFG["hidden"], CFG["n_heads"] * CFG["head_dim"], \
+        CFG["n_kv_heads"] * CFG["head_dim"], CFG["inter"]
+    shapes = [("q", QD, H), ("k", KVD, H), ("v", KVD, H), ("o", H, QD), ("gate", I, H),
+              ("up", I, H), ("down", H, I)]
+    g = torch.Generator(device="cuda").manual_seed(3)
+    layers, host0 = [], None
+    for li in range(L):
+        ws = []
+        for name, n, k in shapes:
+            q = torch.randint(-127, 128, (n, k), generator=g, device="cuda", dtype=torch.int8)
+            s = torch.rand(n, generator=g, device="cuda") * 1e-3 + 1e-4
+            ws.append(ov.Weight.from_device(q, s))
+            if li == 0:
+                host0 = (host0 or []) + [(q.cpu().numpy(), s.cpu().numpy())]
+        ws.append(ov.Weight.concat(ws[0:3]))   # merged q/k/v, as the runner holds it
+        ws.append(ov.Weight.concat(ws[4:6]))   # merged gate/up
+        layers.append(ws)
+    A = {k: torch.randn((M, k), generator=g, device="cuda") for k in (H, QD, I)}
+    acts = {k: ov.s8_nk_quantize(a) for k, a in A.items()}
+    outs = {n: torch.zeros((M, n), device="cuda") for n in (QD, KVD, H, I)}
+    lib = ov.load()
+    st = torch.cuda.current_stream().cuda_stream
+    import ctypes as C
+    qkv_n = (C.c_int64 * 3)(QD, KVD, KVD)
+    qkv_c = (C.c_void_p * 3)(outs[QD].data_ptr(), outs[KVD].data_ptr(), outs[KVD].data_ptr())
+    gu_n = (C.c_int64 * 2)(I, I)
+    gu_c = (C.c_void_p * 2)(outs[I].data_ptr(), outs[I].data_ptr())
+
+    def call(j, ws):
+        if j < 7:
+            name, n, k = shapes[j]
+            aq, asc = acts[k]
+            return lib.ovh_linear_q(M, aq.data_ptr(), asc.data_ptr(), ws[j].handle,
+                                    outs[n].data_ptr(), n, 0, st)
+        aq, asc = acts[H]
+        if j == 7:
+            return lib.ovh_linear_q_sliced(M, aq.data_ptr(), asc.data_ptr(), ws[7].handle, qkv_n,
+                                           qkv_c, 3, st)
+        return lib.ovh_linear_q_sliced(M, aq.data_ptr(), asc.data_ptr(), ws[8].handle, gu_n,
+                                       gu_c, 2, st)
+
+    for ws in layers:
+        for j in range(9):
+            if call(j, ws) != 0:
+                raise RuntimeError("C ABI call failed")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per = {}
+    names = [s[0] for s in shapes] + ["qkv (merged)", "gate/up (merged)"]
+    wbytes = [n * k + 4 * n for _, n, k in shapes]
+    wbytes += [sum(wbytes[0:3]), sum(wbytes[4:6])]
+    for j, nm in enumerate(names):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for ws in layers:
+            call(j, ws)
+        e1.record()
+        torch.cuda.synchronize()
+        per[nm] = e0.elapsed_time(e1) / L
+    wall = time.perf_counter() - t0
+    seven_ms = sum(per[s[0]] for s in shapes)
+    seven_b = sum(wbytes[:7])
+    merged_ms = per["qkv (merged)"] + per["o"] + per["gate/up (merged)"] + per["down"]
+    gbs = seven_b / seven_ms / 1e6
+    for j, nm in enumerate(names):
+        log(f"config 2: {nm:17s} {per[nm] * 1e3:7.2f} us  {wbytes[j] / per[nm] / 1e6:7.1f} GB/s")
+    log(f"config 2: seven projections {seven_ms * 1e3:.1f} us = {gbs:.0f} GB/s; runner's four "
+        f"launches (qkv, o, gate/up, down) {merged_ms * 1e3:.1f} us = "
+        f"{seven_b / merged_ms / 1e6:.0f} GB/s")
+    for ws in layers:
+        for w in ws:
+            w.free()
+    ops = sum(2 * M * n * k for _, n, k in shapes)
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        impl, kind = None, None
+        if oracle.reference_available():
+            try:
+                r = oracle.Reference()
+                if r.vnni_available():
+                    impl, kind = r, "reference"
+            except OSError:
+                impl = None
+        if impl is None:
+            o = oracle.Oracle()
+            if o.fast_available():
+                impl, kind = o, "port"
+        if impl is not None:
+            packs = [impl.pack(q) for q, _ in host0]
+            hacts = {k: impl.quantize(a.cpu().numpy()) for k, a in A.items()}
+            houts = [np.zeros((M, n), np.float32) for _, n, _ in shapes]
+
+            def layer():
+                for j, (name, n, k) in enumerate(shapes):
+                    aq, asc = hacts[k]
+                    impl.linear_q_packed(aq, asc, packs[j][0], packs[j][1], n, k, host0[j][1],
+                                         houts[j])
+            layer()
+            times = []
+            t_end = time.perf_counter() + min(args.cpu_seconds, 10.0)
+            while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+                t1 = time.perf_counter()
+                layer()
+                times.append(time.perf_counter() - t1)
+            sec = statistics.median(times)
+            cpu = {"value": round(seven_b / sec / 1e9, 2), "unit": "GB/s",
+                   "cores": oracle.Oracle().num_threads(), "kind": kind,
+                   "sample": (f"linear_s8_nk_packed_q of the seven projections at M={M} "
+                              f"({'reference gemm.cpp' if kind == 'reference' else 'oracle restatement'}"
+                              f", one layer's weights, warm in the host caches), median of "
+                              f"{len(times)}: {sec * 1e3:.3f} ms = {ops / sec / 1e12:.2f} TOPS"),
+                   "ms_per_step": round(sec * 1e3, 4)}
+    line = bench_line(
+        args, round(gbs, 1), "GB/s", round(seven_ms, 5),
+        {"workload": (f"BASELINE config 2: the seven projections of one layer at M=2x64 through "
+                      f"ovh_linear_q, weights cold from HBM ({L} layers rotated, "
+                      f"{L * seven_b / 1e6:.0f} MB); value = weight bytes / summed kernel time"),
+         "model": "Qwen3-0.6B-shaped layer projections", "global_batch": 2, "seq_len": 64,
+         "parallelism": "single GPU",
+         "per_projection_us": {nm: round(per[nm] * 1e3, 2) for nm in names},
+         "runner_launches_us": round(merged_ms * 1e3, 2),
+         "runner_launches_gbs": round(seven_b / merged_ms / 1e6, 1)},
+        {"bound": "hbm", "kernel": f"gemm16 store, seven projections (M={M}, weights cold)",
+         "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+         "frac": round(gbs / 8000.0, 4), "traffic": None, "avg_ms": round(seven_ms / 7, 5)},
+        cpu, round(wall, 3))
     print(json.dumps(line), flush=True)
 
 
@@ -621,6 +764,9 @@ def main():
         return
     if args.workload == "layer":
         run_layer(args)
+        return
+    if args.workload == "skinny":
+        run_skinny(args)
         return
     cfg = dict(CFG, n_layers=args.layers)
     M = SEQ * CFG_BATCH
