@@ -75,7 +75,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
   // Two stage buffers, each [WT weight row tiles | AT activation row tiles] x SB blocks.
   __shared__ __attribute__((aligned(16))) int8_t smem[2][(WT + AT) * SB * TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index in a scalar register (the slice choice of the epilogue is uniform)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave % WN, wm = wave / WN;
   const int n_tiles = (int)(((int64_t)a.N + BN - 1) / BN);
   const int m_tiles = (a.M + BM - 1) / BM;
@@ -249,24 +250,30 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
   }
   if (MODE == kDumpBlocks) return;
 
-  // Epilogue: column scale, optional residual add, slice-aware store.
+  // Epilogue: column scale, optional residual add, slice-aware store.  Slice
+  // widths are multiples of 64, so the 32 columns of a tile lie in one slice:
+  // the slice is chosen once per tile, in scalar registers.
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wm * TM + j * 32 + (lane & 31);
-    if (m >= a.M) continue;
+  for (int i = 0; i < FN; ++i) {
+    const int n32 = n0 + wn * TN + i * 32;  // wavefront-uniform
+    int s = 0;
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
+    for (int t = 1; t < kMaxSlices; ++t)
+      if (t < a.nslices && n32 >= a.start[t]) s = t;
+    float* const out = a.out[s];
+    const int64_t ld = a.ld[s];
+    const int s0 = a.start[s], s1 = a.start[s + 1];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int m = m0 + wm * TM + j * 32 + (lane & 31);
+      if (m >= a.M) continue;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int nb = n0 + wn * TN + i * 32 + 8 * g + 4 * (lane >> 5);
+        const int nb = n32 + 8 * g + 4 * (lane >> 5);
         if (nb >= a.N) continue;
         const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + nb);
-        int s = 0;
-#pragma unroll
-        for (int t = 1; t < kMaxSlices; ++t)
-          if (t < a.nslices && nb >= a.start[t]) s = t;
-        float* dst = a.out[s] + (int64_t)m * a.ld[s] + (nb - a.start[s]);
-        const int lim = a.start[s + 1] - nb;  // valid columns in this group (>= 1)
+        float* dst = out + (int64_t)m * ld + (nb - s0);
+        const int lim = s1 - nb;  // valid columns in this group (>= 1)
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(f[i][j][4 * g + e], ws[e]);
@@ -595,22 +602,28 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   }
 
   // column scale, optional residual add, slice-aware store: lane holds
-  // n = tile + 4*(l/16) + e (4 consecutive columns) of row m = tile + l%16
+  // n = tile + 4*(l/16) + e (4 consecutive columns) of row m = tile + l%16.
+  // Slice widths are multiples of 64, so the 16 columns of a tile lie in one
+  // slice: the slice is chosen once per tile, in scalar registers.
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
-    if (m >= a.M) continue;
+  for (int i = 0; i < FN; ++i) {
+    const int n16 = n0 + (wn * FN + i) * 16;  // wavefront-uniform
+    int s = 0;
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
-      const int nb = n0 + (wn * FN + i) * 16 + 4 * q;
-      if (nb >= a.N) continue;
-      const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + nb);
-      int s = 0;
+    for (int t = 1; t < kMaxSlices; ++t)
+      if (t < a.nslices && n16 >= a.start[t]) s = t;
+    float* const out = a.out[s];
+    const int64_t ld = a.ld[s];
+    const int s0 = a.start[s], s1 = a.start[s + 1];
+    const int nb = n16 + 4 * q;
+    if (nb >= a.N) continue;
+    const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + nb);
 #pragma unroll
-      for (int t = 1; t < kMaxSlices; ++t)
-        if (t < a.nslices && nb >= a.start[t]) s = t;
-      float* dst = a.out[s] + (int64_t)m * a.ld[s] + (nb - a.start[s]);
-      const int lim = a.start[s + 1] - nb;
+    for (int j = 0; j < FM; ++j) {
+      const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
+      if (m >= a.M) continue;
+      float* dst = out + (int64_t)m * ld + (nb - s0);
+      const int lim = s1 - nb;
       float o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(f[i][j][e], ws[e]);
