@@ -104,6 +104,29 @@ def test_forward_bit_exact_given_attention(oracle, small_lm, split, seq):
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
+@pytest.mark.parametrize("emb_int8", [True, False], ids=["int8_tables", "fp32_tables"])
+def test_many_codebooks_bit_exact_given_attention(oracle, emb_int8):
+    """17 codebooks (more than the embedding kernel's vector path holds in
+    registers, so the per-element path runs) with int8 or fp32 embedding
+    tables: logits identical to the oracle's forward given the device
+    attention."""
+    import ovnative_amd as ov
+    cfg = dict(SMALL, n_layers=1, n_codebooks=17)
+    ts, table = make_lm(13, cfg, emb_int8=emb_int8)
+    ids, am, attn, pos = make_inputs(17, cfg, 2, 45, 9)
+    lm = ov.LM.from_tensors(ts, _cfg(cfg))
+    try:
+        got = lm.forward(ids, am, attn, pos)
+    finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(cfg, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(cfg))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
 def test_full_width_layer_bit_exact_given_attention(oracle):
     """one Qwen3-0.6B-shaped decoder layer (hidden 1024, 16/8
     heads x 128, inter 3072; plus the embeddings and the 8 x 1025 head) on the
