@@ -104,6 +104,22 @@ def test_forward_bit_exact_given_attention(oracle, small_lm, split, seq):
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
+def test_large_batch_bit_exact_given_attention(oracle, small_lm):
+    """M = 4 x 600 = 2400 rows: the runner takes its large-M GEMM tiles (128 x 64,
+    block-by-block stage loop, for q/k/v, the residual projections and the
+    SiLU-fused gate/up) and the logits stay identical to the oracle's forward
+    given the device attention."""
+    ts, table, lm = small_lm
+    ids, am, attn, pos = make_inputs(23, SMALL, 4, 600, 20)
+    got = lm.forward(ids, am, attn, pos)
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(SMALL, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(SMALL))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
 @pytest.mark.parametrize("emb_int8", [True, False], ids=["int8_tables", "fp32_tables"])
 def test_many_codebooks_bit_exact_given_attention(oracle, emb_int8):
     """17 codebooks (more than the embedding kernel's vector path holds in
