@@ -713,9 +713,16 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // 19.4 us); with 2x2 tiles per wavefront its extra live registers cost more
   // than it hides (128x64 at M = 16384, N = 6144: 325 us block by block, 464
   // pipelined).
+  // SiLU-fused gate/up (sweep over 128x64 / 128x32 / 64x64 / 64x32 tiles, N =
+  // 6144, K = 1024, MI355X): up to M = 512 the 32-row tiles give more
+  // wavefronts (M = 128: 8.4 us against 11.4 for 128x64; M = 256: 9.8 against
+  // 11.8 for 64x32 of two wavefronts); from M = 600 the 128x64 tile wins
+  // (17.4 against 18.1 for the next).
   if (mode == kSiluQuant) {
     if (a.Kb % 4) return hipErrorInvalidValue;
     if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);
+    if (M <= 128) return launch_cfg16_silu<128, 32, 2, 2, 4, 2, true>(a, st);
+    if (M <= 512) return launch_cfg16_silu<64, 32, 1, 2, 4, 2, true>(a, st);
     return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, st);
   }
   if (mode != kDumpBlocks && a.Kb % 4 == 0) {

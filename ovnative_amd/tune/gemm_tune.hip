@@ -62,6 +62,27 @@ extern "C" int tune_gemm_silu(int pipe, int M, int N, int Kb, const int8_t* aq, 
               : launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, s);
 }
 
+// SiLU-fused tile variants (wave tiles 64 columns wide): 0/1 = 128x64 block-by-
+// block / pipelined (the product's), 2/3 = 128x32 pipelined / block-by-block,
+// 4 = 64x64 and 5 = 64x32 of two wavefronts, pipelined; activation codes and h
+// tile-major when `tiled`.
+extern "C" int tune_gemm_silu_v(int variant, int M, int N, int Kb, const int8_t* aq,
+                                const float* asc, const int8_t* W, const float* ws, int8_t* hq,
+                                float* hsc, int64_t hKp, int tiled, void* st) {
+  GemmArgs a; a.M = M; a.N = N; a.Kb = Kb; a.Kp = 32 * (int64_t)Kb; a.aq = aq; a.asc = asc;
+  a.W = W; a.ws = ws; a.hq = hq; a.hsc = hsc; a.hKp = hKp; a.a_tiled = tiled; a.h_tiled = tiled;
+  hipStream_t s = (hipStream_t)st;
+  switch (variant) {
+    case 0: return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, s);
+    case 1: return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, s);
+    case 2: return launch_cfg16_silu<128, 32, 2, 2, 4, 2, true>(a, s);
+    case 3: return launch_cfg16_silu<128, 32, 2, 2, 4, 2, false>(a, s);
+    case 4: return launch_cfg16_silu<64, 64, 1, 2, 4, 2, true>(a, s);
+    case 5: return launch_cfg16_silu<64, 32, 1, 2, 4, 2, true>(a, s);
+  }
+  return -1;
+}
+
 extern "C" int tune_gemm(int cfg, int M, int N, int Kb, const int8_t* aq, const float* asc,
                          const int8_t* W, const float* ws, float* C, int accumulate, void* st) {
   return run_cfg(cfg, M, N, Kb, aq, asc, W, ws, C, accumulate, st, 0);
