@@ -47,6 +47,12 @@ static int run_cfg(int cfg, int M, int N, int Kb, const int8_t* aq, const float*
     case 33: return launch_cfg16<128, 64, 4, 2, 4, 3, false>(a, mode, s);
     case 34: return launch_cfg16<32, 32, 2, 2, 4, 4, false>(a, mode, s);
     case 35: return launch_cfg16<64, 32, 2, 2, 4, 3, false>(a, mode, s);
+    // two-wavefront workgroups
+    case 40: return launch_cfg16<32, 32, 1, 2, 4, 2, true>(a, mode, s);
+    case 41: return launch_cfg16<32, 32, 2, 1, 4, 2, true>(a, mode, s);
+    case 42: return launch_cfg16<64, 32, 2, 1, 4, 2, true>(a, mode, s);
+    case 43: return launch_cfg16<64, 32, 1, 2, 4, 2, true>(a, mode, s);
+    case 44: return launch_cfg16<32, 32, 2, 1, 4, 3, true>(a, mode, s);
   }
   return -1;
 }
