@@ -69,9 +69,10 @@ extern "C" int tune_gemm_silu(int pipe, int M, int N, int Kb, const int8_t* aq, 
 }
 
 // SiLU-fused tile variants (wave tiles 64 columns wide): 0/1 = 128x64 block-by-
-// block / pipelined (the product's), 2/3 = 128x32 pipelined / block-by-block,
-// 4 = 64x64 and 5 = 64x32 of two wavefronts, pipelined; activation codes and h
-// tile-major when `tiled`.
+// block / pipelined, 2/3 = 128x32 pipelined / block-by-block, 4 = 64x64 and
+// 5 = 64x32 of two wavefronts, pipelined; 6 = 128x64 with a 3-stage ring, 7/9 =
+// 128x64 with 8-block stages pipelined / block-by-block, 8 = 256x64 of eight
+// wavefronts; activation codes and h tile-major when `tiled`.
 extern "C" int tune_gemm_silu_v(int variant, int M, int N, int Kb, const int8_t* aq,
                                 const float* asc, const int8_t* W, const float* ws, int8_t* hq,
                                 float* hsc, int64_t hKp, int tiled, void* st) {
@@ -85,6 +86,10 @@ extern "C" int tune_gemm_silu_v(int variant, int M, int N, int Kb, const int8_t*
     case 3: return launch_cfg16_silu<128, 32, 2, 2, 4, 2, false>(a, s);
     case 4: return launch_cfg16_silu<64, 64, 1, 2, 4, 2, true>(a, s);
     case 5: return launch_cfg16_silu<64, 32, 1, 2, 4, 2, true>(a, s);
+    case 6: return launch_cfg16_silu<128, 64, 2, 2, 4, 3, true>(a, s);
+    case 7: return launch_cfg16_silu<128, 64, 2, 2, 8, 2, true>(a, s);
+    case 8: return launch_cfg16_silu<256, 64, 4, 2, 4, 2, true>(a, s);
+    case 9: return launch_cfg16_silu<128, 64, 2, 2, 8, 2, false>(a, s);
   }
   return -1;
 }
