@@ -78,14 +78,16 @@ TUNE = os.path.join(HERE, "tune")
 
 
 def build_tools(verbose: bool = False) -> None:
-    """Measurement tools (not part of the library): the tile-sweep harness and the
-    epilogue-ceiling probe, in ovnative_amd/tune/."""
+    """Measurement tools (not part of the library): the tile-sweep harness, the
+    epilogue-ceiling probe and the LDS read-pattern probe, in ovnative_amd/tune/."""
     cmds = [
         [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"], "-shared",
          os.path.join(TUNE, "gemm_tune.hip"),
          "-o", os.path.join(TUNE, "libgemm_tune.so")],
         [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"],
          os.path.join(TUNE, "probe_epilogue.hip"), "-o", os.path.join(TUNE, "probe_epilogue")],
+        [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"],
+         os.path.join(TUNE, "probe_lds.hip"), "-o", os.path.join(TUNE, "probe_lds")],
     ]
     for cmd in cmds:
         if verbose:
