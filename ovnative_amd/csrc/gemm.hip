@@ -738,6 +738,8 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
     return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, st);
   }
+  // the 32x32 kernel reads row-major activation codes only
+  if (a.a_tiled) return hipErrorInvalidValue;
   if (M >= 2048 || (M >= 512 && N >= 6144)) return launch_cfg<128, 64, 2, 2>(a, mode, st);
   if (M >= 256) return launch_cfg<64, 64, 2, 2>(a, mode, st);
   return launch_cfg<32, 32, 1, 1>(a, mode, st);

@@ -614,7 +614,9 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // gate/up epilogue, a hidden width the RMSNorm rows kernel takes): every
   // GEMM then moves its A tiles as 1 KiB contiguous DMA.  Rows are padded to a
   // multiple of 128 (the tallest GEMM tile reads whole tiles).
-  const bool tiled = split && L.silu_fused && H % 256 == 0 && H <= 1024;
+  // tile-major codes need the 16x16 GEMM for every projection that reads them
+  // (K a multiple of 128: H, and inter for down)
+  const bool tiled = split && L.silu_fused && H % 256 == 0 && H <= 1024 && I % 128 == 0;
   const int64_t Tpad = (T + 127) / 128 * 128;
   std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
   int64_t bias_elems = 0, bits_words = 0;

@@ -120,6 +120,28 @@ def test_large_batch_bit_exact_given_attention(oracle, small_lm):
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
+def test_inter_not_multiple_of_128_bit_exact_given_attention(oracle):
+    """inter = 192: the SiLU-fused gate/up still applies (inter % 64 == 0) but the
+    down projection's K = 192 takes the 32x32 GEMM, so the runner keeps its
+    activation codes row-major; logits identical to the oracle's forward given
+    the device attention."""
+    import ovnative_amd as ov
+    cfg = dict(SMALL, n_layers=1, inter=192)
+    ts, table = make_lm(29, cfg)
+    ids, am, attn, pos = make_inputs(31, cfg, 2, 50, 8)
+    lm = ov.LM.from_tensors(ts, _cfg(cfg))
+    try:
+        got = lm.forward(ids, am, attn, pos)
+    finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(cfg, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(cfg))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
 @pytest.mark.parametrize("emb_int8", [True, False], ids=["int8_tables", "fp32_tables"])
 def test_many_codebooks_bit_exact_given_attention(oracle, emb_int8):
     """17 codebooks (more than the embedding kernel's vector path holds in
