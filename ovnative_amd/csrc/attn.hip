@@ -862,7 +862,14 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     }
     if (!valid) return;
     const int64_t col = (int64_t)h * kAttnD + d0;
-    *reinterpret_cast<i32x4*>(sp.aq + act_index(row, col, args.out_stride, sp.aq_tiled)) = codes;
+    if (sp.aq_tiled) {  // the row's 16 codes are two 8-byte pieces of the tile
+      *reinterpret_cast<int2*>(sp.aq + act_index(row, col, args.out_stride, true)) =
+          int2{codes[0], codes[1]};
+      *reinterpret_cast<int2*>(sp.aq + act_index(row, col + 8, args.out_stride, true)) =
+          int2{codes[2], codes[3]};
+    } else {
+      *reinterpret_cast<i32x4*>(sp.aq + row * args.out_stride + col) = codes;
+    }
     if ((threadIdx.x & 1) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(amax, 127.0f);
     return;
   }

@@ -15,14 +15,19 @@
 // wavefront) per 32-clk MFMA, so everything else here is arranged to cost no
 // VALU: operands move as 16-byte chunks in MFMA lane order.
 //
-// Layouts.  A "block tile" is 32 rows x 32 k (one MFMA operand, 1 KiB) stored as
-// 64 chunks of 16 bytes in lane order: chunk l = row l%32, k 16*(l/32)..+15.
-//   weights in HBM : [Npad/32][Kb] block tiles (built once at upload), so a
-//                    wavefront loads a block tile as one contiguous 1 KiB;
+// Layouts.  A "block tile" is 32 rows x 32 k (one MFMA operand, 1 KiB).
+//   weights in HBM : [Npad/32][Kb] block tiles (built once at upload) in the
+//                    interleaved order: 16-row half h at 512 h, k-group
+//                    g = k / 8 % 4 at 128 g, 8 bytes per row (r % 16) * 8, so
+//                    a wavefront loads a block tile as one contiguous 1 KiB and
+//                    the 16x16 kernel's 8-byte fragments are linear;
 //   activations    : row-major int8 [M][Kp] (the quantisers' output), gathered
-//                    into block-tile order on the way to LDS;
-//   LDS            : block tiles in the same order, so fragment reads and
-//                    staging writes are both linear ds_*_b128 (no bank conflicts).
+//                    into row-chunk order on the way to LDS (chunk l = row
+//                    l % 32, k 16 (l / 32)..+15), or, in the runner, tile-major
+//                    in the weights' order (act_index);
+//   LDS            : each operand's tiles in the order it arrives; this
+//                    kernel reads a weight row's 16 bytes as two 8-byte pieces
+//                    and an activation chunk as one 16-byte read.
 // K is staged SB blocks at a time through two LDS buffers, one barrier per
 // stage; global loads run two stages ahead (two register sets), because HBM
 // latency on this part is longer than one stage of epilogue work.
@@ -169,8 +174,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
   auto read_frags = [&](const int8_t* base, int bb, i32x4 (&af)[FN], i32x4 (&bf)[FM])
                         __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
-      af[i] = *reinterpret_cast<const i32x4*>(base + ((wn * FN + i) * SB + bb) * TILE + lane * 16);
+    for (int i = 0; i < FN; ++i) {
+      // weight tile, interleaved layout: row r's k 16h..16h+15 are the 8-byte
+      // pieces of k-groups 2h and 2h + 1, 128 bytes apart
+      const int8_t* tb = base + ((wn * FN + i) * SB + bb) * TILE +
+                         ((lane & 31) >> 4) * 512 + (lane & 15) * 8 + (lane >> 5) * 256;
+      const int64_t lo = *reinterpret_cast<const int64_t*>(tb);
+      const int64_t hi = *reinterpret_cast<const int64_t*>(tb + 128);
+      af[i] = i32x4{(int)lo, (int)(lo >> 32), (int)hi, (int)(hi >> 32)};
+    }
 #pragma unroll
     for (int j = 0; j < FM; ++j)
       bf[j] = *reinterpret_cast<const i32x4*>(base + WT * SB * TILE +
@@ -310,8 +322,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
 // hides the LDS and memory latency behind the VALU epilogue here; the 16-row
 // tiles give narrow-N shapes (N = 1024) several times more wavefronts.
 // Fragment of a 16-row tile (rows 16h..16h+15 of a 32-row block tile): lane l
-// reads 8 bytes of row 16h + l%16 at k = 8*(l/16): chunk (l/32)*32 + row, byte
-// 8*((l/16) & 1) of that 16-byte chunk.
+// reads 8 bytes of row 16h + l%16 at k = 8*(l/16): in the interleaved order
+// (weights, tile-major codes) the bytes 512 h + 8 l, so each 16 lanes read 128
+// contiguous bytes; in the row-chunk order of row-major codes chunk
+// (l/32)*32 + row, byte 8*((l/16) & 1) (two rows 8 apart share a bank there).
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ i32x4 mfma16_i8(int64_t a, int64_t b) {
@@ -413,19 +427,22 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   constexpr int LATER_HI = OPS_HI * (NST - 2), LATER_LO = OPS_LO * (NST - 2);
   constexpr int LATER_LAST = (OPS_LO + SB / 4) * (NST - 2);
   const bool last_wave = wave == NW - 1, hi_wave = EVEN || wave < TILES % NW;
-  // fragment byte offsets inside a block tile (see above)
+  // fragment byte offsets inside a block tile (see above): weights and
+  // tile-major codes in the interleaved layout, lane l's 8 bytes at 512 h + 8 l
+  // (linear); row-major codes as the DMA gathered them, row-chunk order
   const int q = lane >> 4;
-  const int frag = ((q >> 1) * 32 + (lane & 15)) * 16 + (q & 1) * 8;
+  const int frag_rows = ((q >> 1) * 32 + (lane & 15)) * 16 + (q & 1) * 8;
   int aoff[FN], boff[FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int t16 = wn * FN + i;
-    aoff[i] = (t16 >> 1) * SB * TILE + (t16 & 1) * 16 * 16 + frag;
+    aoff[i] = (t16 >> 1) * SB * TILE + (t16 & 1) * 512 + 8 * lane;
   }
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int t16 = wm * FM + j;
-    boff[j] = (WT + (t16 >> 1)) * SB * TILE + (t16 & 1) * 16 * 16 + frag;
+    boff[j] = (WT + (t16 >> 1)) * SB * TILE +
+              (a.a_tiled ? (t16 & 1) * 512 + 8 * lane : (t16 & 1) * 16 * 16 + frag_rows);
   }
 
   f32x4 f[FN][FM];
@@ -747,23 +764,26 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
 
 // ---------------------------------------------------------------------------
 // Weight layout: OVW1 int8 in layout 0 ([N,K]) or 1 ([K,N]) -> block tiles
-// [Npad/32][Kb][64 lanes][16 bytes] with zero padding (rows >= N, k >= K);
-// scales -> [Npad] with zeros.  Load-time only: one thread per 16-byte chunk.
+// [Npad/32][Kb] of 1 KiB in the interleaved order (byte (r / 16) * 512 +
+// (k / 8 % 4) * 128 + (r % 16) * 8 + k % 8 for row r, k of the tile) with zero
+// padding (rows >= N, k >= K); scales -> [Npad] with zeros.  Load-time only:
+// one thread per 16-byte chunk.
 __global__ void weight_layout_kernel(int64_t N, int64_t K, int64_t Npad, int64_t Kb,
                                      const int8_t* __restrict__ src, int layout,
                                      int8_t* __restrict__ dst) {
   const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = Npad / 32 * Kb * 64;
   if (chunk >= total) return;
-  const int lane = (int)(chunk & 63);
+  const int c = (int)(chunk & 63);
   const int64_t tile = chunk >> 6;
   const int64_t rt = tile / Kb, b = tile - rt * Kb;
-  const int64_t n = rt * 32 + (lane & 31);
-  const int64_t k0 = b * 32 + (lane >> 5) * 16;
   int8_t v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int64_t k = k0 + i;
+    // byte 16c + i = piece p = 2c + i/8: row 16 (p / 64) + p % 16, k-group p / 16 % 4
+    const int p = 2 * c + (i >> 3);
+    const int64_t n = rt * 32 + 16 * (p >> 6) + (p & 15);
+    const int64_t k = b * 32 + 8 * ((p >> 4) & 3) + (i & 7);
     v[i] = (n < N && k < K) ? (layout == 0 ? src[n * K + k] : src[k * N + n]) : (int8_t)0;
   }
   int8_t* o = dst + chunk * 16;
@@ -783,8 +803,8 @@ __global__ void weight_to_nk_kernel(int64_t N, int64_t K, int64_t Kb,
   if (idx >= N * K) return;
   const int64_t n = idx / K, k = idx - n * K;
   const int64_t rt = n / 32, b = k / 32;
-  const int lane = (int)(n % 32) + 32 * (int)((k % 32) / 16);
-  dst[idx] = src[((rt * Kb + b) * 64 + lane) * 16 + (k % 16)];
+  const int r = (int)(n % 32), kk = (int)(k % 32);
+  dst[idx] = src[(rt * Kb + b) * 1024 + (r >> 4) * 512 + (kk >> 3) * 128 + (r & 15) * 8 + (kk & 7)];
 }
 
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
@@ -800,8 +820,9 @@ hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int lay
 }
 
 // Block tile c of dst (rows 32c..32c+31) = gate rows 16c..16c+15, then up rows
-// 16c..16c+15; one thread per 16-byte chunk (chunk l of a tile = row l%32,
-// k 16*(l/32)..+15).  Load-time only.
+// 16c..16c+15: in the interleaved tile order each 16-row half is 512
+// contiguous bytes, so dst half h is half c % 2 of gate (h = 0) or up tile
+// c / 2.  One thread per 16-byte chunk.  Load-time only.
 __global__ void weight_interleave16_kernel(int64_t I, int64_t Kb, const int8_t* __restrict__ g,
                                            const int8_t* __restrict__ u, const float* __restrict__ gs,
                                            const float* __restrict__ us, int8_t* __restrict__ dst,
@@ -812,11 +833,13 @@ __global__ void weight_interleave16_kernel(int64_t I, int64_t Kb, const int8_t* 
   const int lane = (int)(chunk & 63);
   const int64_t tile = chunk >> 6;
   const int64_t c = tile / Kb, b = tile - c * Kb;
-  const int r = lane & 31, h = lane >> 5;
-  const int64_t srow = 16 * c + (r & 15);  // row of gate (r < 16) or up
-  const int8_t* src = (r < 16 ? g : u) + (((srow >> 5) * Kb + b) * 64 + (srow & 31) + 32 * h) * 16;
+  const int h = lane >> 5;  // dst half: gate (0) or up (1)
+  const int8_t* src = (h ? u : g) + (((c >> 1) * Kb + b) * 1024) + (c & 1) * 512 + (lane & 31) * 16;
   *reinterpret_cast<i32x4*>(dst + chunk * 16) = *reinterpret_cast<const i32x4*>(src);
-  if (b == 0 && h == 0) ds[32 * c + r] = (r < 16 ? gs : us)[srow];
+  if (b == 0 && lane < 32) {
+    const int r = lane;  // dst row 32c + r: gate row 16c + r (r < 16) or up row 16c + r - 16
+    ds[32 * c + r] = (r < 16 ? gs : us)[16 * c + (r & 15)];
+  }
 }
 
 hipError_t launch_weight_interleave16(const DeviceWeight& gate, const DeviceWeight& up,

@@ -20,13 +20,16 @@ constexpr int kBlockK = 32;  // activation quantisation block (k values)
 __host__ __device__ inline int64_t kb_of(int64_t K) { return (K + 31) / 32; }
 
 // Byte k of row m of int8 activation codes with Kp bytes per row: row-major
-// [M][Kp], or tile-major (the weight tile layout: per 32-row x 32-k tile, 64
-// lanes x 16 bytes, lane = m % 32 + 32 * ((k / 16) % 2); tiles row-tile-major),
-// which the GEMM moves as 1 KiB contiguous DMA.  A store of 4 or 16 bytes at a
-// k aligned to that size stays inside one 16-byte slot.
+// [M][Kp], or tile-major (the weight tile layout: 1 KiB per 32-row x 32-k
+// tile, tiles row-tile-major; inside a tile the 16-row half h = m / 16 % 2 at
+// 512 h, then k-group g = k / 8 % 4 at 128 g, then 8 bytes per row), which the
+// GEMM moves as 1 KiB contiguous DMA and reads as conflict-free 8-byte
+// fragments.  A store of 4 bytes at a k aligned to 4 stays inside one row's
+// 8-byte piece; 16 bytes of a row are two pieces 128 bytes apart.
 __host__ __device__ inline int64_t act_index(int64_t m, int64_t k, int64_t Kp, bool tiled) {
   if (!tiled) return m * Kp + k;
-  return (((m >> 5) * (Kp >> 5) + (k >> 5)) * 64 + (m & 31) + 32 * ((k >> 4) & 1)) * 16 + (k & 15);
+  return ((m >> 5) * (Kp >> 5) + (k >> 5)) * 1024 + ((m >> 4) & 1) * 512 + ((k >> 3) & 3) * 128 +
+         (m & 15) * 8 + (k & 7);
 }
 
 // q = clamp(RNE(v*inv), -127, 127), where a product that x86 cvtps_epi32 cannot
