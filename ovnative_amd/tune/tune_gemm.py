@@ -34,6 +34,7 @@ if argv:
 if tiled:
     cfgs = {k: v for k, v in cfgs.items() if k >= 8}
 shapes = [(600, 6144, 1024), (600, 4096, 1024), (600, 1024, 2048), (600, 1024, 3072), (600, 8192, 1024),
+          (600, 2048, 1024), (600, 3072, 1024),
           (128, 4096, 1024), (128, 6144, 1024), (128, 1024, 2048), (128, 1024, 3072), (128, 2048, 1024), (128, 1024, 1024),
           (256, 3072, 1024), (16384, 6144, 1024), (16384, 1024, 3072)]
 st = torch.cuda.current_stream()

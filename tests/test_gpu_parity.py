@@ -337,3 +337,34 @@ def test_concat_sliced_equals_separate(oracle):
     outs = ov.linear_q_sliced(aq, asc, merged, [2048, 1024, 1024])
     for (q, s), h, o in zip(parts, hs, outs):
         assert np.array_equal(bits(host(o)), bits(host(ov.linear_q(aq, asc, h))))
+
+
+def test_empty_inputs_are_no_ops():
+    """M = 0 (and K = 0 for the quantisers) returns OK without touching any
+    buffer, as the reference's early returns do (cpp/src/backend/cpu/gemm.cpp:710,
+    :724, :761, :779)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(21)
+    q = rng.integers(-127, 128, (64, 96)).astype(np.int8)
+    w = ov.Weight.from_host(q, rng.uniform(1e-3, 1e-2, 64).astype(np.float32))
+    e = torch.empty((0, 96), device="cuda")
+    aq, asc = ov.s8_nk_quantize(e)
+    assert aq.shape == (0, 96) and asc.shape == (0, 3)
+    aq, asc = ov.rmsnorm_quantize(e, torch.ones(96, device="cuda"))
+    assert aq.shape == (0, 96)
+    aq, asc = ov.silu_mul_quantize(e, e)
+    assert aq.shape == (0, 96)
+    assert ov.linear_q(aq, asc, w).shape == (0, 64)
+    assert ov.linear(e, w).shape == (0, 64)
+    assert [o.shape for o in ov.linear_q_sliced(aq, asc, w, [64])] == [(0, 64)]
+    # a zero-width quantiser call writes nothing: a sentinel survives
+    lib = ov.load()
+    A = torch.randn(4, 32, device="cuda")
+    aq = torch.full((4, 32), 7, dtype=torch.int8, device="cuda")
+    asc = torch.full((4, 1), 3.0, device="cuda")
+    for rows, cols in ((0, 32), (4, 0)):
+        assert lib.ovh_s8_nk_quantize(rows, cols, ctypes.c_void_p(A.data_ptr()),
+                                      ctypes.c_void_p(aq.data_ptr()),
+                                      ctypes.c_void_p(asc.data_ptr()), None) == 0
+    torch.cuda.synchronize()
+    assert bool((aq == 7).all()) and bool((asc == 3.0).all())
