@@ -192,9 +192,12 @@ class LmStep:
 def time_residual(cfg: dict, layers: int, M: int, reps: int = 4):
     """The residual GEMM as the step runs it: `layers` o_proj (K = heads*128) and
     `layers` down (K = inter) launches on distinct weights, accumulating into one
-    fp32 [M, hidden] buffer, reps times back to back between one pair of HIP
-    events on the stream they run on.  Returns (ms per launch, int8 ops per
-    launch on average)."""
+    fp32 [M, hidden] buffer, reps passes back to back between one pair of HIP
+    events on the stream they run on.  Each pass has its own set of weights
+    (reps x 140 MB at the LM shape), so, as in the step, where 440 MB of weights
+    go by between two uses of one weight, every launch reads its weight from
+    HBM rather than from the 256 MB last-level cache.  Returns (ms per launch,
+    int8 ops per launch on average)."""
     import torch
     import ovnative_amd as ov
     H, QD, I = cfg["hidden"], cfg["n_heads"] * cfg["head_dim"], cfg["inter"]
@@ -205,8 +208,8 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4):
         s = torch.rand(n, generator=g, device="cuda") * 1e-3 + 1e-4
         return ov.Weight.from_device(q, s)
 
-    wo = [weight(H, QD) for _ in range(layers)]
-    wd = [weight(H, I) for _ in range(layers)]
+    wo = [weight(H, QD) for _ in range(layers * reps)]
+    wd = [weight(H, I) for _ in range(layers * reps)]
     ao = ov.s8_nk_quantize(torch.randn((M, QD), generator=g, device="cuda"))
     ad = ov.s8_nk_quantize(torch.randn((M, I), generator=g, device="cuda"))
     x = torch.zeros((M, H), device="cuda")
@@ -220,17 +223,16 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4):
         calls.append((M, ao[0].data_ptr(), ao[1].data_ptr(), a.handle, x.data_ptr(), H, 1, st))
         calls.append((M, ad[0].data_ptr(), ad[1].data_ptr(), b.handle, x.data_ptr(), H, 1, st))
 
-    def once():
+    def run_all():
         for c in calls:
             if lib.ovh_linear_q(*c) != 0:
                 raise RuntimeError("ovh_linear_q failed")
 
-    once()
+    run_all()  # warm-up; the timed run starts on the set used longest ago
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        once()
+    run_all()
     e1.record()
     torch.cuda.synchronize()
     for w in wo + wd:

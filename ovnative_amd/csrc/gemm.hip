@@ -704,6 +704,8 @@ hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     case kDumpBlocks:
       hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, SB, kDumpBlocks>), grid, block, 0, st, a);
       break;
+    case kSiluQuant:  // the 16x16 kernel's mode only
+      return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -753,6 +755,12 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     // flight (M = 128, weights from HBM, a layer's seven projections: 318 GB/s;
     // 2 stages 225, 4 stages 284)
     if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
+    // o_proj / down at M = 600 (N = 1024): in the LM step each weight comes
+    // cold from HBM (440 MB go by between two uses), and the 3-stage ring takes
+    // the step from 2.65 to 2.48 ms (28 x 2 launches, 15.8 -> 14.4 us each);
+    // with cache-hot weights the 2-stage ring is ~1 us faster per launch.  The
+    // same ring on q/k/v or gate/up made the step slower.
+    if (M >= 512 && M < 1024) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
     return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, st);
   }
   // the 32x32 kernel reads row-major activation codes only
