@@ -736,12 +736,15 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // 6144, K = 1024, MI355X): up to M = 512 the 32-row tiles give more
   // wavefronts (M = 128: 8.4 us against 11.4 for 128x64; M = 256: 9.8 against
   // 11.8 for 64x32 of two wavefronts); from M = 600 the 128x64 tile wins
-  // (17.4 against 18.1 for the next).
+  // with cache-hot weights (17.4 against 18.1 for the next).  At 512 < M < 1024
+  // (the LM step, whose weights come cold from HBM) the 256x64 tile of 8
+  // wavefronts: 16.0 against 17.4 us with cold weights.
   if (mode == kSiluQuant) {
     if (a.Kb % 4) return hipErrorInvalidValue;
     if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);
     if (M <= 128) return launch_cfg16_silu<128, 32, 2, 2, 4, 2, true>(a, st);
     if (M <= 512) return launch_cfg16_silu<64, 32, 1, 2, 4, 2, true>(a, st);
+    if (M < 1024 && a.N % 256 == 0) return launch_cfg16_silu<256, 64, 4, 2, 4, 2, true>(a, st);
     return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, st);
   }
   if (mode != kDumpBlocks && a.Kb % 4 == 0) {
@@ -750,17 +753,26 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     // of 8 wavefronts for wide N at M >= 512 and for every N at M >= 2048.
     if (M >= 2048 || (M >= 512 && N >= 6144))
       return launch_cfg16<128, 64, 4, 2, 4, 2, false>(a, mode, st);
+    // q/k/v at M = 600 with cold weights: 64x32 tiles of 2 wavefronts (13.2 us
+    // against 15.1 for 4 wavefronts, N = 4096, K = 1024)
+    if (M >= 512 && M < 1024 && N >= 2048) return launch_cfg16<64, 32, 2, 1, 4, 2, true>(a, mode, st);
     if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, st);
     // skinny M streams cold weights: a 3-stage ring keeps 2 stages of DMA in
     // flight (M = 128, weights from HBM, a layer's seven projections: 318 GB/s;
     // 2 stages 225, 4 stages 284)
     if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
     // o_proj / down at M = 600 (N = 1024): in the LM step each weight comes
-    // cold from HBM (440 MB go by between two uses), and the 3-stage ring takes
-    // the step from 2.65 to 2.48 ms (28 x 2 launches, 15.8 -> 14.4 us each);
-    // with cache-hot weights the 2-stage ring is ~1 us faster per launch.  The
-    // same ring on q/k/v or gate/up made the step slower.
-    if (M >= 512 && M < 1024) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
+    // cold from HBM (440 MB go by between two uses).  Timed with ~600 MB of
+    // weights rotated (tile-major codes): stages of 8 blocks, 2-stage ring,
+    // 8.7 / 11.3 us at K = 2048 / 3072, against 10.0 / 13.0 for 4-block stages
+    // in a 3-stage ring and 12.1 / 16.4 for 4-block stages in a 2-stage ring
+    // (with cache-hot weights the last is the fastest).  The step: 2.65 ms with
+    // the 2-stage 4-block ring, 2.48-2.54 with the 3-stage, 2.50 with 8-block
+    // stages, 2.48 with these q/k/v and gate/up tiles too.
+    if (M >= 512 && M < 1024) {
+      if (a.Kb % 8 == 0) return launch_cfg16<32, 32, 2, 2, 8, 2, true>(a, mode, st);
+      return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
+    }
     return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, st);
   }
   // the 32x32 kernel reads row-major activation codes only

@@ -172,6 +172,8 @@ def _oracle_linear(oracle, A, q, s, Cin=None):
     (128, 1024, 3072),   # config 2: q, k/v, o, gate/up, down at M = 2 x 64
     (600, 4096, 1024), (600, 6144, 1024), (600, 1024, 3072),  # config 3/4: qkv, gate/up, down
     (1, 1024, 1024), (5, 200, 96), (33, 130, 1000), (65, 64, 32),
+    (520, 192, 1152),    # 512 <= M < 1024, Kb % 8 != 0: the 3-stage ring
+    (700, 2112, 1024),   # 512 <= M < 1024, N >= 2048: 64x32 tiles of 2 wavefronts
 ])
 def test_linear_vs_oracle(oracle, M, N, K):
     import ovnative_amd as ov
