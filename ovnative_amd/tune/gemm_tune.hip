@@ -53,6 +53,11 @@ static int run_cfg(int cfg, int M, int N, int Kb, const int8_t* aq, const float*
     case 42: return launch_cfg16<64, 32, 2, 1, 4, 2, true>(a, mode, s);
     case 43: return launch_cfg16<64, 32, 1, 2, 4, 2, true>(a, mode, s);
     case 44: return launch_cfg16<32, 32, 2, 1, 4, 3, true>(a, mode, s);
+    case 45: return launch_cfg16<32, 32, 2, 1, 8, 2, true>(a, mode, s);
+    case 46: return launch_cfg16<32, 32, 1, 2, 8, 2, true>(a, mode, s);
+    case 47: return launch_cfg16<32, 32, 2, 2, 16, 2, true>(a, mode, s);
+    case 48: return launch_cfg16<64, 32, 2, 1, 8, 2, true>(a, mode, s);
+    case 49: return launch_cfg16<64, 32, 4, 1, 8, 2, true>(a, mode, s);
   }
   return -1;
 }

@@ -34,9 +34,9 @@ def acts(K):
     A = torch.randn(M, K, device='cuda'); aq, asc = ov.s8_nk_quantize(A)
     at = ov.Weight.from_device(aq.view(torch.int8)[:, :K].contiguous(), torch.ones(M, device='cuda'))
     return at, DW.from_address(at.handle.value).q, asc
-for (N, K, acc, cfgs) in [(1024, 2048, 1, [8, 16, 17, 18, 20, 14, 40, 41, 44, 15, 23]),
-                          (1024, 3072, 1, [8, 16, 17, 18, 20, 14, 40, 41, 44, 15, 23]),
-                          (4096, 1024, 0, [9, 23, 21, 15, 13, 12, 16, 8, 42, 43, 19])]:
+for (N, K, acc, cfgs) in [(1024, 2048, 1, [8, 16, 14, 18, 45, 46, 47, 40, 41, 44]),
+                          (1024, 3072, 1, [8, 16, 14, 18, 45, 46, 47, 40, 41, 44]),
+                          (4096, 1024, 0, [9, 42, 43, 48, 49, 13, 15, 12])]:
     ws = weights(N, K); at, ap, asc = acts(K)
     Cc = torch.zeros(M, N, device='cuda'); res = []
     for cfg in cfgs:

@@ -28,7 +28,8 @@ cfgs = {0: '128x128', 1: '64x128', 2: '64x64', 3: '32x64', 4: '128x64', 5: '32x1
         23: 's64x32w4n3', 24: 's64x64w4n4',
         30: 'b32x32w4', 31: 'b64x32w4', 32: 'b128x64w8', 33: 'b128x64w8n3', 34: 'b32x32w4n4',
         35: 'b64x32w4xn3', 40: 's32x32w2m', 41: 's32x32w2n', 42: 's64x32w2', 43: 's64x32w2m',
-        44: 's32x32w2n3'}
+        44: 's32x32w2n3', 45: 's32x32w2nb8', 46: 's32x32w2mb8', 47: 's32x32w4b16', 48: 's64x32w2b8',
+        49: 's64x32w4b8'}
 if argv:
     cfgs = {k: v for k, v in cfgs.items() if str(k) in argv[0].split(',')}
 if tiled:
