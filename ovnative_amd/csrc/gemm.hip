@@ -759,7 +759,11 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, st);
     // skinny M streams cold weights: a 3-stage ring keeps 2 stages of DMA in
     // flight (M = 128, weights from HBM, a layer's seven projections: 318 GB/s;
-    // 2 stages 225, 4 stages 284)
+    // 2 stages 225, 4 stages 284); for N < 2048 (o_proj, down, k, v) stages of
+    // 8 blocks in the 3-stage ring (M = 128, weights cold: o 8.8 -> 7.4 us,
+    // down 11.1 -> 9.5; the merged q/k/v and gate/up were slower with them)
+    if (M < 256 && N < 2048 && a.Kb % 8 == 0)
+      return launch_cfg16<32, 32, 2, 2, 8, 3, true>(a, mode, st);
     if (M < 256) return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
     // o_proj / down at M = 600 (N = 1024): in the LM step each weight comes
     // cold from HBM (440 MB go by between two uses).  Timed with ~600 MB of
