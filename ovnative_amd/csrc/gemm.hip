@@ -756,6 +756,9 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     // q/k/v at M = 600 with cold weights: 64x32 tiles of 2 wavefronts (13.2 us
     // against 15.1 for 4 wavefronts, N = 4096, K = 1024)
     if (M >= 512 && M < 1024 && N >= 2048) return launch_cfg16<64, 32, 2, 1, 4, 2, true>(a, mode, st);
+    // 1024 <= M < 2048, cold weights (M = 1200, N = 4096): 64x64 tiles in a
+    // 3-stage ring, 20.7 against 24.2 us for 64x32 x 4
+    if (M >= 1024 && N >= 2048) return launch_cfg16<64, 64, 2, 2, 4, 3, true>(a, mode, st);
     if (M >= 512 && N >= 2048) return launch_cfg16<64, 32, 4, 1, 4, 2, true>(a, mode, st);
     // skinny M streams cold weights: a 3-stage ring keeps 2 stages of DMA in
     // flight (M = 128, weights from HBM, a layer's seven projections: 318 GB/s;
@@ -777,6 +780,13 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
       if (a.Kb % 8 == 0) return launch_cfg16<32, 32, 2, 2, 8, 2, true>(a, mode, st);
       return launch_cfg16<32, 32, 2, 2, 4, 3, true>(a, mode, st);
     }
+    // the other bands at N < 2048, cold weights (o_proj / down): M = 300
+    // 8-block stages in a 3-stage ring, 7.7 / 9.7 us against 11.6 / 15.9 for
+    // the cache-hot choice below; M = 1200 32x32 tiles of 2 wavefronts, 13.0 /
+    // 18.0 against 13.7 / 20.6
+    if (M >= 256 && M < 512 && N < 2048 && a.Kb % 8 == 0)
+      return launch_cfg16<32, 32, 2, 2, 8, 3, true>(a, mode, st);
+    if (M >= 1024 && N < 2048) return launch_cfg16<32, 32, 2, 1, 4, 2, true>(a, mode, st);
     return launch_cfg16<32, 32, 2, 2, 4, 2, true>(a, mode, st);
   }
   // the 32x32 kernel reads row-major activation codes only

@@ -1,10 +1,10 @@
-"""GEMM tile configs at the LM step's M = 600 shapes with the weights cold, as the
+"""GEMM tile configs at the LM step's shapes (M = 600 by default) with the weights cold, as the
 step reads them: each timed pass walks ~600 MB of distinct weights (more than the
 256 MB last-level cache), activation codes tile-major as the runner holds them.
 Prints the per-launch mean of each config (residual o_proj / down, q/k/v, and
 the SiLU-fused gate/up variants of tune_gemm_silu_v), fastest first.
 
-    python3 ovnative_amd/tune/tune_cold.py
+    python3 ovnative_amd/tune/tune_cold.py [M]
 """
 import ctypes as C, sys, os, math
 R = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
@@ -17,7 +17,7 @@ lib.tune_gemm_silu_v.argtypes = [C.c_int]*4 + [C.c_void_p]*6 + [C.c_int64, C.c_i
 class DW(C.Structure):
     _fields_ = [('N', C.c_int64), ('K', C.c_int64), ('Npad', C.c_int64), ('Kb', C.c_int64), ('Kp', C.c_int64), ('q', C.c_void_p), ('scale', C.c_void_p)]
 st = torch.cuda.current_stream().cuda_stream
-M = 600
+M = int(sys.argv[1]) if len(sys.argv) > 1 else 600
 def weights(N, K):
     n = math.ceil(600e6 / (N * K)); ws = []
     for _ in range(n):

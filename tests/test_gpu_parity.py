@@ -174,6 +174,9 @@ def _oracle_linear(oracle, A, q, s, Cin=None):
     (1, 1024, 1024), (5, 200, 96), (33, 130, 1000), (65, 64, 32),
     (520, 192, 1152),    # 512 <= M < 1024, Kb % 8 != 0: the 3-stage ring
     (700, 2112, 1024),   # 512 <= M < 1024, N >= 2048: 64x32 tiles of 2 wavefronts
+    (300, 1024, 2048),   # 256 <= M < 512, N < 2048: 8-block stages, 3-stage ring
+    (1200, 1024, 3072),  # 1024 <= M < 2048, N < 2048: 32x32 tiles of 2 wavefronts
+    (1200, 4096, 1024),  # 1024 <= M < 2048, N >= 2048: 64x64 tiles, 3-stage ring
 ])
 def test_linear_vs_oracle(oracle, M, N, K):
     import ovnative_amd as ov
