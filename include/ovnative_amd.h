@@ -129,11 +129,39 @@ int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const Ovh
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                int accumulate, void* stream);
 
-/* Debug: the exact int32 dot product of every (m, n, block) computed by the
- * same MFMA code path as ovh_linear_q; out is int32 [M, N, Kb].  The reference
- * keeps these in registers (gemm.cpp:455-474); this exposes them for the
- * bit-exactness check. */
+/* Debug: the exact int32 dot product of every (m, n, block); out is int32
+ * [M, N, Kb].  The reference keeps these in registers (gemm.cpp:455-474); this
+ * exposes them for the bit-exactness check.  They come from the kernel and
+ * tile that ovh_linear_q launches for the same M and weight (same DMA ring,
+ * fragment reads and block products; the per-block values are written out
+ * where ovh_linear_q folds them into the fp32 chain). */
 int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream);
+/* The same with the codes tile-major, the layout the LM runner keeps its
+ * activation codes in: 1 KiB tiles of 32 rows x 32 k, row tile major then
+ * k block; inside a tile byte (m/16 % 2)*512 + (k/8 % 4)*128 + (m % 16)*8 +
+ * k % 8; rows padded to a multiple of 128 (ovh_tiled_codes_bytes).  K must be
+ * a multiple of 128.  No reference counterpart (layout of this library). */
+int ovh_block_dots_tiled(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out,
+                         void* stream);
+int64_t ovh_tiled_codes_bytes(int64_t M, int64_t K);
+
+/* ---- SiLU-gated MLP input ---------------------------------------------------
+ * The reference composes gate/up -> silu*up -> quantise for the down
+ * projection (cpp/src/model/lm.cpp:293-311: linear_s8_nk_packed_q_sliced over
+ * the merged gate/up, then silu_mul_quantize_f32, ops_cpu.cpp:1138-1168).
+ * Here it is one GEMM whose epilogue forms gate and up (the fp32 values the
+ * sliced GEMM would store), silu(gate)*up with the reference's exp256 lane
+ * arithmetic, and its per-32-column block quantisation: hq int8 [M, I] and
+ * hsc fp32 [M, I/32] are byte-identical to silu_mul_quantize_f32's output
+ * (as signed codes, see above) for the same inputs.
+ *
+ * ovh_weight_gate_up builds the operand from gate and up weights [I, K] (I a
+ * multiple of 64; rows interleaved in 16-row groups); that handle is only
+ * accepted by ovh_silu_gate_linear.  K must be a multiple of 128
+ * (OV_ERR_NOT_IMPLEMENTED otherwise). */
+int ovh_weight_gate_up(const OvhWeight* gate, const OvhWeight* up, void* stream, OvhWeight** out);
+int ovh_silu_gate_linear(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* gate_up,
+                         int8_t* hq, float* hsc, void* stream);
 
 /* ---- attention side of a decoder layer (fp32) ------------------------------- */
 

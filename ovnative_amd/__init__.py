@@ -48,6 +48,10 @@ SIGNATURES = {
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
+    "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
+    "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
+    "ovh_weight_gate_up": (_int, [_p, _p, _p, C.POINTER(_p)]),
+    "ovh_silu_gate_linear": (_int, [_i64, _p, _p, _p, _p, _p, _p]),
     "ovh_rope_tables": (_int, [_i64, _p, _int, _f32, _p, _p, _p]),
     "ovh_qk_norm_rope": (_int, [_p, _p, _p, _p, _i64, _int, _int, _int, _p, _p, _f32, _p]),
     "ovh_attention": (_int, [_p, _int, _int, _int, _int, _p, _i64, _p, _p, _i64, _f32, _p,
@@ -313,13 +317,37 @@ def linear(A, w: Weight, C=None, accumulate: bool = False):
     return C
 
 
-def block_dots(aq, w: Weight):
-    """Exact int32 per-(m, n, block) dot products from the MFMA code path."""
+def block_dots(aq, w: Weight, M: int = None, tiled: bool = False):
+    """Exact int32 per-(m, n, block) dot products from the kernel ovh_linear_q
+    launches for the same shape; ``tiled``: aq holds tile-major codes (the LM
+    runner's layout; pass M, since the buffer holds padded rows)."""
     torch = _torch()
-    M = aq.shape[0]
+    M = aq.shape[0] if M is None else M
     out = torch.empty((M, w.N, w.Kb), dtype=torch.int32, device="cuda")
-    _check(load().ovh_block_dots(M, _dptr(aq), w.handle, _dptr(out), _stream()))
+    fn = load().ovh_block_dots_tiled if tiled else load().ovh_block_dots
+    _check(fn(M, _dptr(aq), w.handle, _dptr(out), _stream()))
     return out
+
+
+def gate_up_weight(gate: Weight, up: Weight) -> Weight:
+    """The SiLU-fused operand of gate and up [I, K] (ovh_weight_gate_up)."""
+    h = C.c_void_p()
+    _check(load().ovh_weight_gate_up(gate.handle, up.handle, _stream(), C.byref(h)))
+    return Weight(h.value, 2 * gate.N, gate.K)
+
+
+def silu_gate_linear(aq, asc, gate_up: Weight, out=None):
+    """(hq int8 [M, I], hsc fp32 [M, I/32]) = quantised silu(aq.gate) * (aq.up),
+    byte-identical to linear_q_sliced -> silu_mul_quantize (lm.cpp:293-311)."""
+    torch = _torch()
+    M, I = aq.shape[0], gate_up.N // 2
+    if out is None:
+        out = (torch.empty((M, I), dtype=torch.int8, device="cuda"),
+               torch.empty((M, I // 32), dtype=torch.float32, device="cuda"))
+    hq, hsc = out
+    _check(load().ovh_silu_gate_linear(M, _dptr(aq), _dptr(asc), gate_up.handle, _dptr(hq),
+                                       _dptr(hsc), _stream()))
+    return hq, hsc
 
 
 # ---------------------------------------------------------------------------

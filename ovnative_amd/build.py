@@ -74,30 +74,5 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
-TUNE = os.path.join(HERE, "tune")
-
-
-def build_tools(verbose: bool = False) -> None:
-    """Measurement tools (not part of the library): the tile-sweep harness, the
-    epilogue-ceiling probe and the LDS read-pattern probe, in ovnative_amd/tune/."""
-    cmds = [
-        [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"], "-shared",
-         os.path.join(TUNE, "gemm_tune.hip"),
-         "-o", os.path.join(TUNE, "libgemm_tune.so")],
-        [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"],
-         os.path.join(TUNE, "probe_epilogue.hip"), "-o", os.path.join(TUNE, "probe_epilogue")],
-        [HIPCC, *[f for f in HIP_FLAGS if f != "-fvisibility=hidden"],
-         os.path.join(TUNE, "probe_lds.hip"), "-o", os.path.join(TUNE, "probe_lds")],
-    ]
-    for cmd in cmds:
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-        if r.returncode:
-            print(r.stdout.decode(errors="replace"), file=sys.stderr)
-            raise RuntimeError(f"hipcc failed: {cmd[-1]}")
-
-
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
-    build_tools(verbose="-v" in sys.argv)

@@ -1196,10 +1196,14 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   // per-lane offsets into one KV head's tiles are 32-bit, in bytes
   // (vt_cols / 32 blocks x 8 KiB)
   if (256 * (uint64_t)sp.vt_cols >= (1ull << 32) || sp.vt_cols % 32 != 0) return hipErrorInvalidValue;
-  const int QT = kAttnWaves * kAttnQ / args.group;  // query rows per long-form workgroup
+  // The long form holds the G heads of a KV group in its 4 wavefronts, so it
+  // needs 4 % G == 0 (then QT >= 32; any other G, up to n_heads, takes the
+  // short form below, which has no limit on G).
+  const bool lds_ok = args.group > 0 && kAttnWaves % args.group == 0;
+  const int QT = lds_ok ? kAttnWaves * kAttnQ / args.group : 1;  // query rows per long-form workgroup
   const int lds_qtiles = (max_rows + QT - 1) / QT;
-  const int lds_tasks = args.n_segs * (args.n_heads / args.group) * lds_qtiles;
-  if (lds_tasks >= kLdsMinTasks && kAttnWaves % args.group == 0) {
+  const int lds_tasks = lds_ok ? args.n_segs * (args.n_heads / args.group) * lds_qtiles : 0;
+  if (lds_ok && lds_tasks >= kLdsMinTasks) {
     // a chip's worth of long-form workgroups: K/V blocks shared through LDS
     // by 128 query-head rows
     const int qtiles = lds_qtiles;

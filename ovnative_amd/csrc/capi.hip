@@ -63,6 +63,9 @@ int new_weight(int64_t N, int64_t K, OvhWeight** out) {
 
 int check_gemm_operands(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w) {
   if (!w) return fail(OV_ERR_INVALID_ARG, "weight handle is null");
+  if (w->silu_pair)
+    return fail(OV_ERR_INVALID_ARG, "weight is an interleaved gate/up operand: use "
+                                    "ovh_silu_gate_linear");
   if (M > 0x7fffffff || w->w.N > 0x7fffffff)
     return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
   if (!aq || !asc) return fail(OV_ERR_INVALID_ARG, "aq/asc must be device pointers");
@@ -89,7 +92,8 @@ namespace ovh {
 int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
                         OvhWeight** out) {
   *out = nullptr;
-  if (!gate || !up || gate->w.N != up->w.N || gate->w.K != up->w.K || gate->w.N % 64 != 0)
+  if (!gate || !up || gate->silu_pair || up->silu_pair || gate->w.N != up->w.N ||
+      gate->w.K != up->w.K || gate->w.N % 64 != 0)
     return fail(OV_ERR_INVALID_ARG, "interleave: gate/up need equal shapes, rows a multiple of 64");
   OvhWeight* h = nullptr;
   const int rc = new_weight(2 * gate->w.N, gate->w.K, &h);
@@ -99,6 +103,7 @@ int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t 
     ovh_weight_free(h);
     return hip_fail(e, "weight interleave");
   }
+  h->silu_pair = true;
   *out = h;
   return OV_OK;
 }
@@ -235,7 +240,7 @@ int ovh_weight_concat(const OvhWeight* const* parts, int n_parts, void* stream, 
   int64_t N = 0;
   const int64_t K = parts[0] ? parts[0]->w.K : 0;
   for (int i = 0; i < n_parts; ++i) {
-    if (!parts[i] || parts[i]->w.K != K || parts[i]->w.N % 64 != 0)
+    if (!parts[i] || parts[i]->silu_pair || parts[i]->w.K != K || parts[i]->w.N % 64 != 0)
       return fail(OV_ERR_INVALID_ARG, "concat: parts need equal K and N a multiple of 64");
     N += parts[i]->w.N;
   }
@@ -357,16 +362,71 @@ int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t 
   return rc;
 }
 
-int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream) {
+namespace {
+int block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream,
+               bool tiled) {
   if (M <= 0) return OV_OK;
   int rc = check_gemm_operands(M, aq, reinterpret_cast<const float*>(aq), w);
   if (rc != OV_OK) return rc;
   if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  if (tiled && w->w.Kb % 4 != 0)
+    return fail(OV_ERR_INVALID_ARG, "block_dots_tiled: K must be a multiple of 128");
   ovh::GemmArgs a = base_args(M, aq, nullptr, w);
   a.asc = nullptr;
+  a.a_tiled = tiled;
   a.start[1] = (int)w->w.N;
   a.dump = out;
   OVH_HIP(ovh::launch_gemm(a, ovh::kDumpBlocks, as_stream(stream)), "gemm launch");
+  return OV_OK;
+}
+}  // namespace
+
+int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream) {
+  return block_dots(M, aq, w, out, stream, false);
+}
+
+int ovh_block_dots_tiled(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out,
+                         void* stream) {
+  return block_dots(M, aq, w, out, stream, true);
+}
+
+int64_t ovh_tiled_codes_bytes(int64_t M, int64_t K) {
+  return (M <= 0 || K <= 0) ? 0 : (M + 127) / 128 * 128 * ovh::kb_of(K) * 32;
+}
+
+// ---- SiLU-fused gate/up ------------------------------------------------------
+
+int ovh_weight_gate_up(const OvhWeight* gate, const OvhWeight* up, void* stream, OvhWeight** out) {
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  return ovh::weight_interleave16(gate, up, as_stream(stream), out);
+}
+
+int ovh_silu_gate_linear(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* gate_up,
+                         int8_t* hq, float* hsc, void* stream) {
+  if (M <= 0) return OV_OK;
+  if (!gate_up) return fail(OV_ERR_INVALID_ARG, "weight handle is null");
+  if (!gate_up->silu_pair)
+    return fail(OV_ERR_INVALID_ARG, "silu_gate_linear: the weight must come from ovh_weight_gate_up");
+  if (M > 0x7fffffff || gate_up->w.N > 0x7fffffff)
+    return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
+  if (!aq || !asc || !hq || !hsc) return fail(OV_ERR_INVALID_ARG, "null device pointer");
+  if (!aligned16(aq) || ((uintptr_t)hq & 3u) != 0)
+    return fail(OV_ERR_INVALID_ARG, "aq must be 16-byte and hq 4-byte aligned");
+  if (gate_up->w.Kb % 4 != 0)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "silu_gate_linear: K must be a multiple of 128");
+  ovh::GemmArgs a;
+  a.M = (int)M;
+  a.N = (int)gate_up->w.N;
+  a.Kb = (int)gate_up->w.Kb;
+  a.Kp = gate_up->w.Kp;
+  a.aq = aq;
+  a.asc = asc;
+  a.W = gate_up->w.q;
+  a.ws = gate_up->w.scale;
+  a.hq = hq;
+  a.hsc = hsc;
+  a.hKp = gate_up->w.N / 2;  // I, a multiple of 64
+  OVH_HIP(ovh::launch_gemm(a, ovh::kSiluQuant, as_stream(stream)), "silu gate/up launch");
   return OV_OK;
 }
 

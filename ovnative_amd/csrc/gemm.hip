@@ -359,6 +359,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   constexpr int STAGE = SCL + BM * SB * 4;
   constexpr int TPW = (TILES + NW - 1) / NW;
   constexpr bool EVEN = TILES % NW == 0;
+  // kDumpBlocks writes each block's int32 products and takes no scales (asc
+  // may be null): no scale DMA, so every wavefront's op count is its tiles'
+  constexpr bool DUMP = MODE == kDumpBlocks;
+  constexpr int SOPS = DUMP ? 0 : SB / 4;  // scale DMA ops of the last wavefront per stage
   __shared__ __attribute__((aligned(16))) int8_t smem[NST][STAGE];
 
   // wave index in a scalar register: the DMA slots and the wait below branch on it
@@ -394,8 +398,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       step[t] = SB * 32;
     }
   }
-  const float* ssrc;
-  {
+  const float* ssrc = nullptr;
+  if (!DUMP) {
     int row = m0 + lane;
     row = row < a.M ? row : a.M - 1;
     ssrc = a.asc + (int64_t)row * Kb;
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[t] + s * step[t]),
                                          (lds_void_t*)(base + idx * TILE), 16, 0, 0);
     }
-    if (wave == NW - 1 && lane < BM) {
+    if (!DUMP && wave == NW - 1 && lane < BM) {
 #pragma unroll
       for (int c = 0; c < SB / 4; ++c)
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc + s * SB + 4 * c),
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   // smaller one would also wait for part of the next stage.
   constexpr int OPS_HI = TPW, OPS_LO = EVEN ? TPW : TPW - 1;
   constexpr int LATER_HI = OPS_HI * (NST - 2), LATER_LO = OPS_LO * (NST - 2);
-  constexpr int LATER_LAST = (OPS_LO + SB / 4) * (NST - 2);
+  constexpr int LATER_LAST = (OPS_LO + SOPS) * (NST - 2);
   const bool last_wave = wave == NW - 1, hi_wave = EVEN || wave < TILES % NW;
   // fragment byte offsets inside a block tile (see above): weights and
   // tile-major codes in the interleaved layout, lane l's 8 bytes at 512 h + 8 l
@@ -502,16 +506,30 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 #pragma unroll
         for (int j = 0; j < FM; ++j) acc[bb][i][j] = mfma16_i8(af[bb][i], bf[bb][j]);
   };
-  auto epilogue = [&]() __attribute__((always_inline)) {
+  // kDumpBlocks: block b's int32 product of output (m, n) to dump[(m N + n) Kb + b]
+  auto dump_block = [&](const i32x4& p, int i, int j, int b) __attribute__((always_inline)) {
+    const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
+    const int nb = n0 + (wn * FN + i) * 16 + 4 * q;
+    if (m >= a.M) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (nb + e < a.N) a.dump[((int64_t)m * a.N + nb + e) * Kb + b] = p[e];
+  };
+  auto epilogue = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
     for (int bb = 0; bb < SB; ++bb)
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
+        for (int j = 0; j < FM; ++j) {
+          if constexpr (DUMP) {
+            dump_block(acc[bb][i][j], i, j, s * SB + bb);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            f[i][j][e] = fmaf((float)acc[bb][i][j][e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+            for (int e = 0; e < 4; ++e)
+              f[i][j][e] = fmaf((float)acc[bb][i][j][e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+          }
+        }
   };
 
 #pragma unroll
@@ -528,14 +546,14 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       // finished before the barrier
       if (s + NST < nstages) issue(s + NST);
       read_stage(s + 1, sc_next);
-      epilogue();
+      epilogue(s);
       products();
 #pragma unroll
       for (int c = 0; c < SB / 4; ++c)
 #pragma unroll
         for (int j = 0; j < FM; ++j) sc[c][j] = sc_next[c][j];
     }
-    epilogue();
+    epilogue(nstages - 1);
   } else {
     for (int s = 0; s < nstages; ++s) {
       wait_stage(s);
@@ -563,13 +581,19 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
             const i32x4 p = mfma16_i8(a1[i], b1[j]);
+            if constexpr (DUMP) {
+              dump_block(p, i, j, s * SB + bb);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              f[i][j][e] = fmaf((float)p[e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+              for (int e = 0; e < 4; ++e)
+                f[i][j][e] = fmaf((float)p[e], sc[bb >> 2][j][bb & 3], f[i][j][e]);
+            }
           }
       }
     }
   }
+
+  if constexpr (DUMP) return;
 
   if constexpr (MODE == kSiluQuant) {
     // Tiles 4p..4p+3 of the wavefront are gate, up, gate, up rows of 32
@@ -673,6 +697,9 @@ hipError_t launch_cfg16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   if (mode == kAccumulate)
     hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumulate, PIPE>), grid, block, 0,
                        st, a);
+  else if (mode == kDumpBlocks)
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kDumpBlocks, PIPE>), grid, block, 0,
+                       st, a);
   else
     hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kStore, PIPE>), grid, block, 0, st, a);
   return hipGetLastError();
@@ -747,7 +774,9 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     if (M < 1024 && a.N % 256 == 0) return launch_cfg16_silu<256, 64, 4, 2, 4, 2, true>(a, st);
     return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, st);
   }
-  if (mode != kDumpBlocks && a.Kb % 4 == 0) {
+  // kDumpBlocks takes the tile the store and residual modes take for the same
+  // shape (the kernel differs only after the block products)
+  if (a.Kb % 4 == 0) {
     // 16x16 wave tiles (sweep on MI355X, LM shapes at M = 128 / 600 / 16384):
     // many small workgroups for the skinny and N = 1024 shapes, 128x64 tiles
     // of 8 wavefronts for wide N at M >= 512 and for every N at M >= 2048.

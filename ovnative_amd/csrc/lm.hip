@@ -932,7 +932,9 @@ int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_te
     }
     L->st = L->own_st;
   }
-  L->silu_fused = cfg->inter % 64 == 0;
+  // the SiLU-fused gate/up GEMM takes K = hidden in 4-block stages (hidden a
+  // multiple of 128); other widths compose the sliced GEMM and silu_mul_quantize
+  L->silu_fused = cfg->inter % 64 == 0 && cfg->hidden % 128 == 0;
   int rc = OV_OK;
   if (hipMalloc(reinterpret_cast<void**>(&L->d_overflow), sizeof(uint32_t)) != hipSuccess ||
       hipMemset(L->d_overflow, 0, sizeof(uint32_t)) != hipSuccess)

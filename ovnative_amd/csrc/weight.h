@@ -8,6 +8,9 @@
 
 struct OvhWeight {
   ovh::DeviceWeight w;
+  // rows interleaved gate/up in 16-row groups (weight_interleave16): only the
+  // SiLU-fused operator takes such a weight
+  bool silu_pair = false;
 };
 
 namespace ovh {

@@ -15,6 +15,8 @@ SMALL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, inte
 # the mask id the unconditional row carries in its text slots).
 FULL1 = dict(n_layers=1, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, inter=3072,
              vocab=2048, audio_vocab=1025, n_codebooks=8, rms_eps=1e-6, rope_theta=1e6)
+# all 28 layers at the real widths (440 MB of int8 weights).
+FULL28 = dict(FULL1, n_layers=28)
 
 
 def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True):

@@ -136,6 +136,7 @@ def _segments(rng, seg_rows, masked):
     ([700], 4, 4, False),         # KV group of 1
     ([1, 33, 64, 65], 4, 2, True),
     ([7], 2, 2, False),
+    ([40, 33], 256, 1, True),     # a KV group of 256 heads (more than a workgroup's rows)
 ])
 def test_attention_vs_oracle(oracle, seg_rows, nh, nkv, masked, split):
     import ovnative_amd as ov

@@ -21,7 +21,7 @@ Bars:
 import numpy as np
 import pytest
 
-from lm_fixture import FULL1, SMALL, make_inputs, make_lm
+from lm_fixture import FULL1, FULL28, SMALL, make_inputs, make_lm
 
 pytestmark = pytest.mark.gpu
 
@@ -129,6 +129,28 @@ def test_inter_not_multiple_of_128_bit_exact_given_attention(oracle):
     cfg = dict(SMALL, n_layers=1, inter=192)
     ts, table = make_lm(29, cfg)
     ids, am, attn, pos = make_inputs(31, cfg, 2, 50, 8)
+    lm = ov.LM.from_tensors(ts, _cfg(cfg))
+    try:
+        got = lm.forward(ids, am, attn, pos)
+    finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(cfg, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(cfg))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
+def test_hidden_not_multiple_of_128_bit_exact_given_attention(oracle):
+    """hidden = 192 (64 mod 128): the SiLU-fused gate/up needs K in 4-block
+    stages, so the runner composes the sliced gate/up GEMM and silu_mul_quantize
+    instead, with row-major codes; the forward runs (it used to fail at the first
+    launch) and its logits equal the oracle's forward given the device attention."""
+    import ovnative_amd as ov
+    cfg = dict(SMALL, n_layers=1, hidden=192, inter=256)
+    ts, table = make_lm(37, cfg)
+    ids, am, attn, pos = make_inputs(41, cfg, 2, 40, 7)
     lm = ov.LM.from_tensors(ts, _cfg(cfg))
     try:
         got = lm.forward(ids, am, attn, pos)
@@ -375,3 +397,84 @@ def test_graph_replays_match_eager(small_lm):
     finally:
         lm.set_graphs(True)
     assert np.array_equal(got, eager)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 4 at full size: 28 layers, hidden 1024, 16/8 heads, inter
+# 3072, head 8 x 1025, the tts.cpp CFG batch B = 2, S = 300 (40 text + 260
+# audio positions), and the 32-step decode.
+
+# The reference's int8 quality gate (cpp/tests/test_lm.cpp:229-233): cosine >
+# 0.99999, mean |delta| < 0.15, argmax agreement >= 80 %.
+INT8_COS, INT8_MEAN, INT8_AGREE = 0.99999, 0.15, 0.80
+
+
+@pytest.fixture(scope="module")
+def full_lm():
+    import ovnative_amd as ov
+    ts, table = make_lm(101, FULL28)
+    lm = ov.LM.from_tensors(ts, _cfg(FULL28))
+    yield ts, table, lm
+    lm.close()
+
+
+def test_config4_forward_bit_exact_given_attention(oracle, full_lm):
+    """The full 28-layer LM at B = 2, S = 300: the runner's logits equal, bit for
+    bit, the oracle's forward (lm.cpp:339-401) with the device attention
+    substituted; against the pure oracle (fp32 attention of the reference's
+    order) the logits pass the reference's own int8 gate."""
+    ts, table, lm = full_lm
+    ids, am, attn, pos = make_inputs(103, FULL28, 2, 300, 40)
+    got = lm.forward(ids, am, attn, pos)                  # [B, C, S, V]
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(FULL28, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(FULL28))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+    want = oracle.lm_forward(FULL28, table, ids, am, segs, pos.reshape(-1))
+    d = flat.astype(np.float64) - want
+    cos = float((flat.astype(np.float64) * want).sum() /
+                (np.linalg.norm(flat.astype(np.float64)) * np.linalg.norm(want.astype(np.float64))))
+    mean = float(np.abs(d).mean())
+    agree = float((flat.reshape(-1, V).argmax(1) == want.reshape(-1, V).argmax(1)).mean())
+    print(f"config 4 logits vs the pure oracle: max rel {_rel(flat, want):.3g}, mean |d| "
+          f"{mean:.3g}, cosine {cos:.9f}, argmax agreement {agree:.4f}")
+    assert cos > INT8_COS and mean < INT8_MEAN and agree >= INT8_AGREE
+
+
+def test_config4_generate_32_steps(full_lm):
+    """ovh_lm_generate at config 4 (S = 300: 40 text positions, 260 target
+    frames, 8 codebooks, 32 steps, the reference's default options) against the
+    restated host loop of tts.cpp:165-364 driven by the same runner's forward
+    and device sampler: identical tokens."""
+    import oracle
+    import ovnative_amd as ov
+    ts, table, lm = full_lm
+    Cb, V = FULL28["n_codebooks"], FULL28["audio_vocab"]
+    S, T = 300, 260
+    rng = np.random.default_rng(107)
+    prompt = np.full((Cb, S), V - 1, np.int64)
+    prompt[0, :S - T] = rng.integers(0, FULL28["vocab"], S - T)
+    am = np.zeros(S, np.uint8)
+    am[S - T:] = 1
+    opts = dict(num_steps=32, guidance_scale=2.0, t_shift=0.1, layer_penalty=5.0,
+                position_temperature=5.0, seed=1234)
+    got = lm.generate(prompt, am, T, ov.GenOptions(**opts))
+    plane = S * Cb * V * 4
+
+    def step(ids, amask, attn, pos):
+        lm.set_device_sampling(True)
+        try:
+            lm.forward(ids, amask, attn, pos, host_logits=False)
+            base = lm.last_logits_ptr()
+            return lm.sample(base, S, base + plane, S, T, opts["guidance_scale"],
+                             opts["layer_penalty"])
+        finally:
+            lm.set_device_sampling(False)
+
+    want = oracle.run_sampling(step, prompt, am, T, Cb, V, num_steps=32, guidance=2.0,
+                               t_shift=0.1, layer_penalty=5.0, position_temperature=5.0,
+                               seed=1234)
+    assert np.all(got != V - 1)
+    assert np.array_equal(got, want)

@@ -373,3 +373,123 @@ def test_empty_inputs_are_no_ops():
                                       ctypes.c_void_p(asc.data_ptr()), None) == 0
     torch.cuda.synchronize()
     assert bool((aq == 7).all()) and bool((asc == 3.0).all())
+
+
+# ---------------------------------------------------------------------------
+# per-block int32 of the production kernel, and the SiLU-fused gate/up operator
+
+def tile_major(aq: np.ndarray, M: int) -> np.ndarray:
+    """Row-major codes [M, Kp] -> the runner's tile-major layout (1 KiB tiles of
+    32 rows x 32 k; inside a tile (m/16 % 2)*512 + (k/8 % 4)*128 + (m%16)*8 + k%8),
+    rows padded with zeros to a multiple of 128."""
+    Kp = aq.shape[1]
+    Mp = (M + 127) // 128 * 128
+    a = np.zeros((Mp, Kp), np.int8)
+    a[:M] = aq[:M]
+    # [mt, h, r, kb, g, e] -> [mt, kb, h, g, r, e]
+    t = a.reshape(Mp // 32, 2, 16, Kp // 32, 4, 8).transpose(0, 3, 1, 4, 2, 5)
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def _brute_blocks(aq_rows: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """Integer brute force: [rows, N, Kb] int64 block dot products."""
+    Kp = aq_rows.shape[1]
+    N, K = q.shape
+    w = np.zeros((N, Kp), np.int64)
+    w[:, :K] = q
+    w = w.reshape(N, Kp // 32, 32)
+    return np.stack([(a.astype(np.int64).reshape(1, Kp // 32, 32) * w).sum(axis=2)
+                     for a in aq_rows])
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (256, 3072, 1024),                      # BASELINE config 1
+    (600, 4096, 1024), (600, 6144, 1024),   # config 3: q/k/v, gate/up
+    (600, 1024, 3072), (600, 1024, 2048),   # config 3: down, o_proj
+    (128, 1024, 3072), (128, 2048, 1024),   # config 2 (3-stage ring tiles)
+    (2400, 1024, 1024), (1200, 4096, 1024),  # 128x64 and 64x64 tiles
+])
+@pytest.mark.parametrize("tiled", [False, True], ids=["rowmajor", "tilemajor"])
+def test_block_dots_production_kernel(oracle, M, N, K, tiled):
+    """ovh_block_dots / _tiled run the kernel and tile ovh_linear_q launches for
+    the shape (K a multiple of 128: the 16x16 kernel): its per-block int32 sums
+    equal integer brute force on sampled rows (gemm.cpp:455-474), with the codes
+    row-major (the C ABI's format) and tile-major (the runner's)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(M + 3 * N + 7 * K + tiled)
+    A, Wf = _rand_problem(rng, M, N, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    aq_h = host(aq)
+    if tiled:
+        t = tile_major(aq_h, M)
+        assert t.size == ov.load().ovh_tiled_codes_bytes(M, K)
+        blocks = ov.block_dots(dev(t), w, M=M, tiled=True)
+    else:
+        blocks = ov.block_dots(aq, w)
+    rows = np.sort(np.concatenate([rng.choice(M, min(M, 20), replace=False), [M - 1]]))
+    got = blocks[torch.from_numpy(rows).cuda()].cpu().numpy()
+    want = _brute_blocks(aq_h[rows], q)
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+@pytest.mark.parametrize("M", [1, 100, 128, 256, 600, 2400])
+def test_silu_gate_linear_vs_oracle(oracle, M):
+    """ovh_silu_gate_linear (gate/up GEMM with silu*up and its quantisation in the
+    epilogue) == the reference's composition: the sliced gate/up GEMM, then
+    silu_mul_quantize_f32 (lm.cpp:293-311), byte for byte, in every tile band of
+    the fused kernel; also equal to the device's own unfused composition."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(40 + M)
+    I, K = 3072, 1024
+    A = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    qg, sg = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    qu, su = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    wg, wu = ov.Weight.from_host(qg, sg), ov.Weight.from_host(qu, su)
+    gu = ov.gate_up_weight(wg, wu)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    hq, hsc = ov.silu_gate_linear(aq, asc, gu)
+    hq, hsc = host(hq), host(hsc)
+    gate = _oracle_linear(oracle, A, qg, sg)
+    up = _oracle_linear(oracle, A, qu, su)
+    hq_r, hsc_r = oracle.silu_mul_quantize(gate, up)
+    assert np.array_equal(hq, u8_to_s8(hq_r, I))
+    assert np.array_equal(bits(hsc), bits(hsc_r))
+    merged = ov.Weight.concat([wg, wu])
+    g_d, u_d = ov.linear_q_sliced(aq, asc, merged, [I, I])
+    hq2, hsc2 = ov.silu_mul_quantize(g_d, u_d)
+    assert np.array_equal(host(hq2), hq) and np.array_equal(bits(host(hsc2)), bits(hsc))
+
+
+def test_silu_gate_linear_small_width_and_errors(oracle):
+    """I = 320 (N = 640, not a multiple of 256) at M = 37; a plain weight is
+    refused by the fused operator and the interleaved one by the plain GEMMs;
+    K = 96 is not covered (OV_ERR_NOT_IMPLEMENTED)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(77)
+    M, I, K = 37, 320, 256
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    qg, sg = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.05).astype(np.float32))
+    qu, su = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.05).astype(np.float32))
+    wg, wu = ov.Weight.from_host(qg, sg), ov.Weight.from_host(qu, su)
+    gu = ov.gate_up_weight(wg, wu)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    hq, hsc = ov.silu_gate_linear(aq, asc, gu)
+    hq_r, hsc_r = oracle.silu_mul_quantize(_oracle_linear(oracle, A, qg, sg),
+                                           _oracle_linear(oracle, A, qu, su))
+    assert np.array_equal(host(hq), u8_to_s8(hq_r, I))
+    assert np.array_equal(bits(host(hsc)), bits(hsc_r))
+    with pytest.raises(ov.InvalidArgument):
+        ov.silu_gate_linear(aq, asc, wg)
+    with pytest.raises(ov.InvalidArgument):
+        ov.linear_q(aq, asc, gu)
+    with pytest.raises(ov.InvalidArgument):
+        ov.Weight.concat([gu, wg])
+    q96 = rng.integers(-127, 128, (64, 96)).astype(np.int8)
+    s96 = np.full(64, 1e-2, np.float32)
+    g96 = ov.gate_up_weight(ov.Weight.from_host(q96, s96), ov.Weight.from_host(q96, s96))
+    aq96, asc96 = ov.s8_nk_quantize(dev(rng.standard_normal((5, 96)).astype(np.float32)))
+    with pytest.raises(ov.OvhError) as e:
+        ov.silu_gate_linear(aq96, asc96, g96)
+    assert e.value.code == ov.OV_ERR_NOT_IMPLEMENTED
