@@ -404,9 +404,48 @@ def test_graph_replays_match_eager(small_lm):
 # 3072, head 8 x 1025, the tts.cpp CFG batch B = 2, S = 300 (40 text + 260
 # audio positions), and the 32-step decode.
 
-# The reference's int8 quality gate (cpp/tests/test_lm.cpp:229-233): cosine >
-# 0.99999, mean |delta| < 0.15, argmax agreement >= 80 %.
-INT8_COS, INT8_MEAN, INT8_AGREE = 0.99999, 0.15, 0.80
+# The reference's int8 quality gate (cpp/tests/test_lm.cpp:229-233): mean
+# |delta| < 0.15 and argmax agreement >= 80 % are used as they are.  Its cosine
+# > 0.99999 was set for a trained checkpoint against fp32 logits; on this random
+# 28-layer checkpoint (logits ~0.5 in magnitude) no attention with another
+# summation order meets it: the oracle's forward with attention computed in
+# float64 and rounded once (more accurate than either) sits at cosine 0.99992
+# from the pure oracle.  So the cosine gate is relative to that noise floor.
+INT8_MEAN, INT8_AGREE, COS_FLOOR_FACTOR = 0.15, 0.80, 2.0
+
+
+def _attention_f64(cfg):
+    """Attention in float64 (softmax of q k^T * scale + bias, then p v), output
+    rounded once to fp32, fully masked rows 0: an order-free stand-in for the
+    reference's attention_head_f32 (ops_cpu.cpp:907-943)."""
+    NH, NKV, D = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    scale = np.float64(np.float32(1.0) / np.sqrt(np.float32(D)))
+
+    def run(q, k, v, segs):
+        out = np.zeros_like(q)
+        for bias, r, r0, k0 in segs:
+            for h in range(NH):
+                kv = h // (NH // NKV)
+                Q = q[r0:r0 + r, h * D:(h + 1) * D].astype(np.float64)
+                K = k[k0:k0 + r, kv * D:(kv + 1) * D].astype(np.float64)
+                Vv = v[k0:k0 + r, kv * D:(kv + 1) * D].astype(np.float64)
+                sc = Q @ K.T * scale
+                if bias is not None:
+                    sc = sc + bias
+                m = sc.max(axis=1, keepdims=True)
+                p = np.exp(sc - m)
+                o = (p / p.sum(axis=1, keepdims=True)) @ Vv
+                o[m[:, 0] < -1e29] = 0.0
+                out[r0:r0 + r, h * D:(h + 1) * D] = o.astype(np.float32)
+        return out
+    return run
+
+
+def _logit_stats(got, want, V):
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    cos = float((g * w).sum() / (np.linalg.norm(g) * np.linalg.norm(w)))
+    return dict(max_rel=_rel(got, want), mean=float(np.abs(g - w).mean()), cos=cos,
+                agree=float((got.reshape(-1, V).argmax(1) == want.reshape(-1, V).argmax(1)).mean()))
 
 
 @pytest.fixture(scope="module")
@@ -422,7 +461,9 @@ def test_config4_forward_bit_exact_given_attention(oracle, full_lm):
     """The full 28-layer LM at B = 2, S = 300: the runner's logits equal, bit for
     bit, the oracle's forward (lm.cpp:339-401) with the device attention
     substituted; against the pure oracle (fp32 attention of the reference's
-    order) the logits pass the reference's own int8 gate."""
+    order) the logits pass the reference's int8 gate for mean error and argmax
+    agreement, and their cosine is within 2x of the checkpoint's noise floor
+    (the same forward with float64 attention)."""
     ts, table, lm = full_lm
     ids, am, attn, pos = make_inputs(103, FULL28, 2, 300, 40)
     got = lm.forward(ids, am, attn, pos)                  # [B, C, S, V]
@@ -433,14 +474,12 @@ def test_config4_forward_bit_exact_given_attention(oracle, full_lm):
                                attention=_device_attention(FULL28))
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
     want = oracle.lm_forward(FULL28, table, ids, am, segs, pos.reshape(-1))
-    d = flat.astype(np.float64) - want
-    cos = float((flat.astype(np.float64) * want).sum() /
-                (np.linalg.norm(flat.astype(np.float64)) * np.linalg.norm(want.astype(np.float64))))
-    mean = float(np.abs(d).mean())
-    agree = float((flat.reshape(-1, V).argmax(1) == want.reshape(-1, V).argmax(1)).mean())
-    print(f"config 4 logits vs the pure oracle: max rel {_rel(flat, want):.3g}, mean |d| "
-          f"{mean:.3g}, cosine {cos:.9f}, argmax agreement {agree:.4f}")
-    assert cos > INT8_COS and mean < INT8_MEAN and agree >= INT8_AGREE
+    floor = oracle.lm_forward(FULL28, table, ids, am, segs, pos.reshape(-1),
+                              attention=_attention_f64(FULL28))
+    st, fl = _logit_stats(flat, want, V), _logit_stats(floor, want, V)
+    print(f"config 4 logits vs the pure oracle: {st}; float64 attention vs the pure oracle: {fl}")
+    assert st["mean"] < INT8_MEAN and st["agree"] >= INT8_AGREE
+    assert 1.0 - st["cos"] <= COS_FLOOR_FACTOR * (1.0 - fl["cos"])
 
 
 def test_config4_generate_32_steps(full_lm):
