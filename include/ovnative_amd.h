@@ -128,6 +128,18 @@ int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const Ovh
  * quantise A (fp32 [M,K]) into a library-owned workspace, then ovh_linear_q. */
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                int accumulate, void* stream);
+/* ovh_linear without any allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The codes and scales
+ * go to a fixed 16 MiB device array per GPU (held from the first call on that
+ * GPU until the process ends), so M * (Kp + 4 * Kb) plus up to 255 bytes of
+ * alignment must fit in 16 MiB (e.g. M <= 14560 at K = 1024, M <= 4850 at
+ * K = 3072); larger calls return OV_ERR_INVALID_ARG.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * threads) race; order them on one stream.  Same results, bit for bit, as
+ * ovh_linear. */
+int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+                       int accumulate, void* stream);
 
 /* Debug: the exact int32 dot product of every (m, n, block); out is int32
  * [M, N, Kb].  The reference keeps these in registers (gemm.cpp:455-474); this

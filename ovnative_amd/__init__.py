@@ -47,6 +47,7 @@ SIGNATURES = {
     "ovh_linear_q": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
+    "ovh_linear_noalloc": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),

@@ -8,6 +8,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/ovnative_amd.h"
@@ -383,6 +384,64 @@ int block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, vo
 
 int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out, void* stream) {
   return block_dots(M, aq, w, out, stream, false);
+}
+
+// ---- allocation-free linear -------------------------------------------------
+// ovh_linear quantises A into a stream-ordered allocation; this variant puts
+// the codes and scales in a fixed device array instead.  Each device holds its
+// own copy of `scratch` (a file-scope device array) from the first call on it
+// until the process ends; its device address is looked up once per device with
+// that device current and kept in g_scratch.  In host code the array's name is
+// not a device address: only the looked-up pointer reaches kernels.
+}  // extern "C"
+
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  OVH_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "linear_noalloc: device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    OVH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(OV_ERR_INTERNAL, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return OV_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+                       int accumulate, void* stream) {
+  if (M <= 0) return OV_OK;
+  if (!w || !A) return fail(OV_ERR_INVALID_ARG, "null argument");
+  // codes [M][Kp] at offset 0, scales [M][Kb] at the next 256-byte boundary;
+  // the quantiser writes every byte of both (K-tail padding included), so
+  // nothing has to start at zero
+  const size_t code_bytes = ((size_t)M * (size_t)w->w.Kp + 255) & ~(size_t)255;
+  const size_t need = code_bytes + sizeof(float) * (size_t)M * (size_t)w->w.Kb;
+  if (M > ((int64_t)1 << 31) || need > kNoAllocScratchBytes)
+    return fail(OV_ERR_INVALID_ARG,
+                "linear_noalloc: M * (Kp + 4 * Kb) = " + std::to_string(need) +
+                    " bytes exceeds the 16 MiB scratch (use ovh_linear)");
+  void* base = nullptr;
+  int rc = scratch_of_current_device(&base);
+  if (rc != OV_OK) return rc;
+  int8_t* aq = static_cast<int8_t*>(base);
+  float* asc = reinterpret_cast<float*>(static_cast<char*>(base) + code_bytes);
+  rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
+  if (rc == OV_OK) rc = ovh_linear_q(M, aq, asc, w, C, ldc, accumulate, stream);
+  return rc;
 }
 
 int ovh_block_dots_tiled(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out,
