@@ -116,6 +116,12 @@ int ovh_silu_mul_quantize(int64_t M, int64_t K, const float* gate, const float* 
  * C = C + P with P rounded first (the reference's "keep mul/add separate"). */
 int ovh_linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
                  int64_t ldc, int accumulate, void* stream);
+/* ovh_linear_q with the codes aq tile-major (the LM runner's layout, described
+ * at ovh_block_dots_tiled; a buffer of ovh_tiled_codes_bytes(M, K)); the same
+ * results bit for bit.  K must be a multiple of 128.  No reference counterpart
+ * (layout of this library); it runs the GEMM the way the runner does. */
+int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                       float* C, int64_t ldc, int accumulate, void* stream);
 /* linear_s8_nk_packed_q_sliced (ov_gemm.h:105-111, gemm.cpp:776-827): one launch
  * over a concatenated weight, slice s (N = slice_n[s], a positive multiple of
  * 64, summing to the weight's N) written to slice_c[s] with leading dimension

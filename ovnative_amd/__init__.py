@@ -46,6 +46,7 @@ SIGNATURES = {
     "ovh_silu_mul_quantize": (_int, [_i64, _i64, _p, _p, _p, _p, _p]),
     "ovh_linear_q": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
+    "ovh_linear_q_tiled": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_noalloc": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
@@ -291,6 +292,29 @@ def linear_q(aq, asc, w: Weight, C=None, accumulate: bool = False):
         C = torch.zeros((M, w.N), dtype=torch.float32, device="cuda")
     _check(load().ovh_linear_q(M, _dptr(aq), _dptr(asc), w.handle, _dptr(C), C.shape[1],
                                int(bool(accumulate)), _stream()))
+    return C
+
+
+def tile_major(aq, M: int = None):
+    """Row-major codes [M, Kp] (device) -> the runner's tile-major layout (1 KiB
+    tiles of 32 rows x 32 k; inside a tile (m/16 % 2)*512 + (k/8 % 4)*128 +
+    (m%16)*8 + k%8), rows zero-padded to a multiple of 128."""
+    torch = _torch()
+    M = aq.shape[0] if M is None else M
+    Kp = aq.shape[1]
+    Mp = (M + 127) // 128 * 128
+    a = torch.zeros((Mp, Kp), dtype=torch.int8, device=aq.device)
+    a[:M] = aq[:M]
+    return a.view(Mp // 32, 2, 16, Kp // 32, 4, 8).permute(0, 3, 1, 4, 2, 5).contiguous().view(-1)
+
+
+def linear_q_tiled(aq_tiled, asc, w: Weight, M: int, C=None, accumulate: bool = False):
+    """linear_q on tile-major codes (tile_major), as the LM runner runs it."""
+    torch = _torch()
+    if C is None:
+        C = torch.zeros((M, w.N), dtype=torch.float32, device="cuda")
+    _check(load().ovh_linear_q_tiled(M, _dptr(aq_tiled), _dptr(asc), w.handle, _dptr(C),
+                                     C.shape[1], int(bool(accumulate)), _stream()))
     return C
 
 

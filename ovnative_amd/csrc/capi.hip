@@ -334,6 +334,13 @@ int ovh_linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight*
   return ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), false);
 }
 
+int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
+                       float* C, int64_t ldc, int accumulate, void* stream) {
+  if (M > 0 && w && w->w.Kb % 4 != 0)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_tiled: K must be a multiple of 128");
+  return ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), true);
+}
+
 int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                         const int64_t* slice_n, float* const* slice_c, int n_slices,
                         void* stream) {

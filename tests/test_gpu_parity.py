@@ -434,6 +434,29 @@ def test_block_dots_production_kernel(oracle, M, N, K, tiled):
     assert np.array_equal(got.astype(np.int64), want)
 
 
+@pytest.mark.parametrize("M,N,K", [(600, 1024, 2048), (600, 1024, 3072), (128, 4096, 1024),
+                                   (37, 320, 256)])
+def test_linear_q_tiled_equals_rowmajor(oracle, M, N, K):
+    """ovh_linear_q_tiled (the runner's tile-major codes) gives ovh_linear_q's
+    bits, store and residual forms; the device layout helper matches the
+    host restatement of the layout."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(M + N + K)
+    A, Wf = _rand_problem(rng, M, N, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    t = ov.tile_major(aq)
+    assert np.array_equal(host(t), tile_major(host(aq), M))
+    assert np.array_equal(bits(host(ov.linear_q_tiled(t, asc, w, M))),
+                          bits(host(ov.linear_q(aq, asc, w))))
+    Cin = rng.standard_normal((M, N)).astype(np.float32)
+    c1, c2 = dev(Cin), dev(Cin)
+    ov.linear_q(aq, asc, w, c1, accumulate=True)
+    ov.linear_q_tiled(t, asc, w, M, c2, accumulate=True)
+    assert np.array_equal(bits(host(c1)), bits(host(c2)))
+
+
 @pytest.mark.parametrize("M", [1, 100, 128, 256, 600, 2400])
 def test_silu_gate_linear_vs_oracle(oracle, M):
     """ovh_silu_gate_linear (gate/up GEMM with silu*up and its quantisation in the
