@@ -147,6 +147,23 @@ int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t 
 int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                        int accumulate, void* stream);
 
+/* ---- fp32 linear (Mat's fp32 branch) ----------------------------------------
+ * Mat::mul / mul_add on an fp32 weight (cpp/src/model/mat.cpp:11-13, :40-42 ->
+ * linear_f32_ld, cpp/src/backend/cpu/gemm.cpp:884-905): C = A W (accumulate 0)
+ * or C = C + A W (accumulate 1, the sum rounded separately), A fp32 [M, K], W
+ * fp32 [K, N].  The reference's default int8 checkpoint keeps the audio head
+ * in this form (tools/convert_weights.py --int8-keep audio_heads).  Computed on
+ * the f16 matrix cores from hi/lo splits of power-of-two-scaled operands
+ * (hi*hi + hi*lo + lo*hi, fp32 sums): not the reference's bits (its fma chain
+ * over k), a few fp32 ulps of sum_k |A W| from them.  The weight is uploaded
+ * once from host memory, OVW1 layout 0 ([N, K]) or 1 ([K, N], the reference's
+ * fp32 encoding); ovh_linear_f32 allocates its split activations stream-ordered. */
+int ovh_weight_upload_f32(int64_t N, int64_t K, const float* w, int layout, void* stream,
+                          OvhWeight** out);
+int ovh_weight_is_f32(const OvhWeight* w);
+int ovh_linear_f32(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+                   int accumulate, void* stream);
+
 /* Debug: the exact int32 dot product of every (m, n, block); out is int32
  * [M, N, Kb].  The reference keeps these in registers (gemm.cpp:455-474); this
  * exposes them for the bit-exactness check.  They come from the kernel and

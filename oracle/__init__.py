@@ -68,6 +68,7 @@ class Oracle:
             "ovo_silu_mul_quantize_u8": (None, [_i64, _i64, _p, _p, _p, _p]),
             "ovo_block_dots": (None, [_i64, _i64, _i64, _p, _p, _p]),
             "ovo_linear_q": (None, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, C.c_int]),
+            "ovo_linear_f32": (None, [_i64, _i64, _i64, _p, _p, _p, _i64, C.c_int]),
             "ovo_packed_bytes": (_i64, [_i64, _i64]),
             "ovo_wsum_elems": (_i64, [_i64, _i64]),
             "ovo_pack": (None, [_i64, _i64, _p, _p, _p]),
@@ -166,6 +167,18 @@ class Oracle:
         wscale = np.ascontiguousarray(wscale, dtype=np.float32)
         self.lib.ovo_linear_q(M, N, K, _ptr(aq), _ptr(asc), _ptr(W), _ptr(wscale), _ptr(C),
                               C.shape[1], int(bool(accumulate)))
+        return C
+
+    def linear_f32(self, A, W_kn, C=None, accumulate=False):
+        """linear_f32_ld (gemm.cpp:884-905): C (+)= A W, W stored [K, N] fp32."""
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        W_kn = np.ascontiguousarray(W_kn, dtype=np.float32)
+        K, N = W_kn.shape
+        M = A.shape[0]
+        C = np.zeros((M, N), np.float32) if C is None else \
+            np.array(C, dtype=np.float32, copy=True, order="C")
+        self.lib.ovo_linear_f32(M, N, K, _ptr(A), _ptr(W_kn), _ptr(C), C.shape[1],
+                                int(bool(accumulate)))
         return C
 
     def linear(self, A, W, wscale, C=None, accumulate=False):
@@ -349,6 +362,13 @@ class Oracle:
             up = lq(aq, asc, *lin(p + "mlp.up_proj.weight"))
             aq, asc = self.silu_mul_quantize(gate, up)
             x = lq(aq, asc, *lin(p + "mlp.down_proj.weight"), C=x, accumulate=True)
+        head, head_s, head_t = g("audio_heads.weight")
+        if head_s is None:
+            # the fp32 head of the reference's default int8 checkpoint, stored
+            # [K, N] (lm.cpp:383-385: rmsnorm_f32, then Mat's fp32 branch)
+            if not head_t:
+                raise ValueError("audio_heads.weight: an fp32 head must be stored [K, N]")
+            return self.linear_f32(self.rmsnorm(x, g("llm.norm.weight")[0], eps), head)
         aq, asc = self.rmsnorm_quantize(x, g("llm.norm.weight")[0], eps)
         return self._linear_fast(aq, asc, *lin("audio_heads.weight"))
 
@@ -375,6 +395,7 @@ class Reference:
             "ovref_linear_packed_q": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
                                                 C.c_int]),
             "ovref_linear_packed": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _p, _p, C.c_int]),
+            "ovref_linear_f32": (C.c_int, [_i64, _i64, _i64, _p, _p, _p, _i64, C.c_int]),
             "ovref_linear_packed_q_sliced": (C.c_int, [_i64, _i64, _p, _p, _p, _p, _p, _p, _p,
                                                        C.c_int]),
             "ovref_qk_norm_rope": (None, [_p, _p, _p, _p, _i64, C.c_int, C.c_int, C.c_int, _p,
@@ -584,6 +605,18 @@ class Reference:
             self.linear_q_packed(aq, asc, packed, wsum, N, K, ones, C)
             out[:, :, b] = C.astype(np.int32)
         return out
+
+    def linear_f32(self, A, W_kn, C=None, accumulate=False):
+        A = np.ascontiguousarray(A, dtype=np.float32)
+        W_kn = np.ascontiguousarray(W_kn, dtype=np.float32)
+        K, N = W_kn.shape
+        M = A.shape[0]
+        C = np.zeros((M, N), np.float32) if C is None else \
+            np.array(C, dtype=np.float32, copy=True, order="C")
+        if self.lib.ovref_linear_f32(M, N, K, _ptr(A), _ptr(W_kn), _ptr(C), C.shape[1],
+                                     int(bool(accumulate))):
+            raise RuntimeError("reference linear_f32_ld failed")
+        return C
 
     def linear_q_sliced(self, aq, asc, W_slices, scale_slices):
         """Merged [sum N, K] matrix with one C per slice (gemm.cpp:776-827)."""

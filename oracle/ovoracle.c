@@ -21,6 +21,8 @@
  *   ovo_block_dots             cpp/src/backend/cpu/gemm.cpp:455-474 (acc - 128*wsum per block)
  *   ovo_linear_q               cpp/src/backend/cpu/gemm.cpp:432-504 (vnni_tile_at epilogue)
  *   ovo_pack / ovo_linear_q_packed   the same arithmetic on AVX-512 VNNI, for timing
+ *   ovo_linear_f32             cpp/src/backend/cpu/gemm.cpp:64-110, 283-330, 884-905
+ *                              (linear_f32_ld: Mat's fp32 branch, the fp32 audio head)
  *
  * "The reference's arithmetic" means the reference as its own build compiles it:
  * g++ -O3 -std=c++17.  For C++, GCC's default is -ffp-contract=fast, so some
@@ -317,6 +319,29 @@ OVO_API void ovo_linear_q(int64_t M, int64_t N, int64_t K, const uint8_t* aq, co
       float o = f * wscale[n];
       if (accumulate) o = o + C[m * ldc + n];
       C[m * ldc + n] = o;
+    }
+  }
+}
+
+/* gemm.cpp:884-905 -> linear_f32_ld_avx2 :283-330: C[i, j] (+)= sum_k A[i, k] W[k, j],
+ * W stored [K, N].  Every output is one fma chain over k from +0, in k order:
+ * columns in full groups of 8 in micro_f32_8x8 (:64-110), and the N % 8 column
+ * tail in the lambda's scalar loop "acc += a[k] * W[k*N+j]" (:297-303), which
+ * the reference binary also fuses (it is compiled inside the avx2/fma function
+ * with GCC's default -ffp-contract=fast).  accumulate: C_old + acc, rounded
+ * once more. */
+OVO_API void ovo_linear_f32(int64_t M, int64_t N, int64_t K, const float* A, const float* W,
+                            float* C, int64_t ldc, int accumulate) {
+  if (M <= 0 || N <= 0 || K <= 0) return;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t i = 0; i < M; ++i) {
+    for (int64_t j = 0; j < N; ++j) {
+      const float* a = A + i * K;
+      float acc = 0.f;
+      for (int64_t k = 0; k < K; ++k)
+        acc = OVO_PLANT == 10 ? acc + a[k] * W[k * N + j] : fmaf(a[k], W[k * N + j], acc);
+      float* c = C + i * ldc + j;
+      *c = accumulate ? *c + acc : acc;
     }
   }
 }

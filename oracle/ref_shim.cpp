@@ -57,6 +57,12 @@ REF_API int ovref_linear_packed_q(int64_t M, int64_t N, int64_t K, const uint8_t
     return 0;
   } catch (const std::exception&) { return -1; }
 }
+// linear_f32_ld (gemm.cpp:884-905): Mat's fp32 branch, W [K, N].
+REF_API int ovref_linear_f32(int64_t M, int64_t N, int64_t K, const float* A, const float* W,
+                             float* C, int64_t ldc, int accumulate) {
+  try { ov::linear_f32_ld(M, N, K, A, W, C, ldc, accumulate != 0); return 0; }
+  catch (const std::exception&) { return -1; }
+}
 REF_API int ovref_linear_packed(int64_t M, int64_t N, int64_t K, const float* A,
                                 const int8_t* packed, const int32_t* wsum, const float* scale,
                                 float* C, int accumulate) {

@@ -49,6 +49,9 @@ SIGNATURES = {
     "ovh_linear_q_tiled": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_noalloc": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
+    "ovh_weight_upload_f32": (_int, [_i64, _i64, _p, _int, _p, C.POINTER(_p)]),
+    "ovh_weight_is_f32": (_int, [_p]),
+    "ovh_linear_f32": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
@@ -225,6 +228,16 @@ class Weight:
         return cls(h.value, N, K)
 
     @classmethod
+    def from_host_f32(cls, w, layout: int = 1) -> "Weight":
+        """fp32 weight: layout 1 = [K, N] (the reference's fp32 encoding), 0 = [N, K]."""
+        import numpy as np
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        N, K = (w.shape if layout == 0 else w.shape[::-1])
+        h = C.c_void_p()
+        _check(load().ovh_weight_upload_f32(N, K, w.ctypes.data, layout, _stream(), C.byref(h)))
+        return cls(h.value, N, K)
+
+    @classmethod
     def concat(cls, parts) -> "Weight":
         arr = (C.c_void_p * len(parts))(*[p.handle.value for p in parts])
         h = C.c_void_p()
@@ -339,6 +352,17 @@ def linear(A, w: Weight, C=None, accumulate: bool = False):
         C = torch.zeros((M, w.N), dtype=torch.float32, device="cuda")
     _check(load().ovh_linear(M, _dptr(A), w.handle, _dptr(C), C.shape[1], int(bool(accumulate)),
                              _stream()))
+    return C
+
+
+def linear_f32(A, w: Weight, C=None, accumulate: bool = False):
+    """Mat's fp32 branch: C (+)= A W on the f16 matrix cores (hi/lo splits)."""
+    torch = _torch()
+    M = A.shape[0]
+    if C is None:
+        C = torch.zeros((M, w.N), dtype=torch.float32, device="cuda")
+    _check(load().ovh_linear_f32(M, _dptr(A), w.handle, _dptr(C), C.shape[1],
+                                 int(bool(accumulate)), _stream()))
     return C
 
 

@@ -880,13 +880,6 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     *reinterpret_cast<f32x4*>(dst + j) = f32x4{ov[j], ov[j + 1], ov[j + 2], ov[j + 3]};
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 // ---------------------------------------------------------------------------
 // Long-sequence form of the split-f16 attention.  In the form above every

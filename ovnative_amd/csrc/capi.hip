@@ -67,6 +67,7 @@ int check_gemm_operands(int64_t M, const int8_t* aq, const float* asc, const Ovh
   if (w->silu_pair)
     return fail(OV_ERR_INVALID_ARG, "weight is an interleaved gate/up operand: use "
                                     "ovh_silu_gate_linear");
+  if (w->f32) return fail(OV_ERR_INVALID_ARG, "weight is fp32: use ovh_linear_f32");
   if (M > 0x7fffffff || w->w.N > 0x7fffffff)
     return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
   if (!aq || !asc) return fail(OV_ERR_INVALID_ARG, "aq/asc must be device pointers");
@@ -93,7 +94,8 @@ namespace ovh {
 int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
                         OvhWeight** out) {
   *out = nullptr;
-  if (!gate || !up || gate->silu_pair || up->silu_pair || gate->w.N != up->w.N ||
+  if (!gate || !up || gate->silu_pair || up->silu_pair || gate->f32 || up->f32 ||
+      gate->w.N != up->w.N ||
       gate->w.K != up->w.K || gate->w.N % 64 != 0)
     return fail(OV_ERR_INVALID_ARG, "interleave: gate/up need equal shapes, rows a multiple of 64");
   OvhWeight* h = nullptr;
@@ -111,6 +113,41 @@ int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t 
 }  // namespace ovh
 
 namespace ovh {
+int weight_upload_f32(int64_t N, int64_t K, const float* wsrc, int layout, hipStream_t st,
+                      OvhWeight** out) {
+  *out = nullptr;
+  if (N <= 0 || K <= 0) return fail(OV_ERR_INVALID_ARG, "weight dims must be positive");
+  if (layout != 0 && layout != 1) return fail(OV_ERR_INVALID_ARG, "layout must be 0 (nk) or 1 (kn)");
+  if (!wsrc) return fail(OV_ERR_INVALID_ARG, "weight is null");
+  auto* h = new (std::nothrow) OvhWeight();
+  if (!h) return fail(OV_ERR_INTERNAL, "out of host memory");
+  h->f32 = true;
+  h->w.N = N;
+  h->w.K = K;
+  F32Weight& fw = h->fw;
+  fw.N = N;
+  fw.K = K;
+  fw.Np = (N + 127) / 128 * 128;
+  fw.Ks = (K + 15) / 16;
+  const size_t plane = sizeof(_Float16) * (size_t)f32_plane_halves(N, K);
+  float* staging = nullptr;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&fw.hi), plane);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&fw.lo), plane);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&fw.scale), sizeof(float) * (size_t)fw.Np);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&staging), sizeof(float) * (size_t)(N * K));
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(staging, wsrc, sizeof(float) * (size_t)(N * K), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = launch_f32_weight(N, K, staging, layout, fw, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);  // staging is freed below
+  if (staging) (void)hipFree(staging);
+  if (e != hipSuccess) {
+    ovh_weight_free(h);
+    return hip_fail(e, "fp32 weight upload");
+  }
+  *out = h;
+  return OV_OK;
+}
+
 int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
              int64_t ldc, int accumulate, hipStream_t st, bool a_tiled) {
   if (M <= 0) return OV_OK;
@@ -241,7 +278,8 @@ int ovh_weight_concat(const OvhWeight* const* parts, int n_parts, void* stream, 
   int64_t N = 0;
   const int64_t K = parts[0] ? parts[0]->w.K : 0;
   for (int i = 0; i < n_parts; ++i) {
-    if (!parts[i] || parts[i]->silu_pair || parts[i]->w.K != K || parts[i]->w.N % 64 != 0)
+    if (!parts[i] || parts[i]->silu_pair || parts[i]->f32 || parts[i]->w.K != K ||
+        parts[i]->w.N % 64 != 0)
       return fail(OV_ERR_INVALID_ARG, "concat: parts need equal K and N a multiple of 64");
     N += parts[i]->w.N;
   }
@@ -277,14 +315,63 @@ void ovh_weight_free(OvhWeight* h) {
   if (!h) return;
   if (h->w.q) (void)hipFree(h->w.q);
   if (h->w.scale) (void)hipFree(h->w.scale);
+  if (h->fw.hi) (void)hipFree(h->fw.hi);
+  if (h->fw.lo) (void)hipFree(h->fw.lo);
+  if (h->fw.scale) (void)hipFree(h->fw.scale);
   delete h;
 }
 
+int ovh_weight_upload_f32(int64_t N, int64_t K, const float* w, int layout, void* stream,
+                          OvhWeight** out) {
+  if (!out) return fail(OV_ERR_INVALID_ARG, "out is null");
+  return ovh::weight_upload_f32(N, K, w, layout, as_stream(stream), out);
+}
+
+int ovh_linear_f32(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
+                   int accumulate, void* stream) {
+  if (M <= 0) return OV_OK;
+  if (!w || !A || !C) return fail(OV_ERR_INVALID_ARG, "null argument");
+  if (!w->f32) return fail(OV_ERR_INVALID_ARG, "linear_f32: the weight is not fp32");
+  if (M > 0x7fffffff || w->w.N > 0x7fffffff)
+    return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
+  if (ldc < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldc < N");
+  const hipStream_t st = as_stream(stream);
+  const ovh::F32Weight& fw = w->fw;
+  const size_t plane = sizeof(_Float16) * (size_t)ovh::f32_plane_halves(M, fw.K);
+  const size_t rows = (size_t)((M + 127) / 128 * 128);
+  char* ws = nullptr;
+  OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(&ws), 2 * plane + sizeof(float) * rows, st),
+          "hipMallocAsync(linear_f32)");
+  ovh::GemmF32Args a;
+  a.M = (int)M;
+  a.N = (int)fw.N;
+  a.Ks = fw.Ks;
+  _Float16* hi = reinterpret_cast<_Float16*>(ws);
+  _Float16* lo = reinterpret_cast<_Float16*>(ws + plane);
+  float* sc = reinterpret_cast<float*>(ws + 2 * plane);
+  a.ahi = hi;
+  a.alo = lo;
+  a.ascale = sc;
+  a.whi = fw.hi;
+  a.wlo = fw.lo;
+  a.wscale = fw.scale;
+  a.C = C;
+  a.ldc = ldc;
+  a.accumulate = accumulate != 0;
+  hipError_t e = ovh::launch_f32_split(M, fw.K, A, fw.Ks, hi, lo, sc, st);
+  if (e == hipSuccess) e = ovh::launch_gemm_f32(a, st);
+  (void)hipFreeAsync(ws, st);
+  if (e != hipSuccess) return hip_fail(e, "linear_f32 launch");
+  return OV_OK;
+}
+
 int64_t ovh_weight_n(const OvhWeight* w) { return w ? w->w.N : 0; }
+int ovh_weight_is_f32(const OvhWeight* w) { return w && w->f32 ? 1 : 0; }
 int64_t ovh_weight_k(const OvhWeight* w) { return w ? w->w.K : 0; }
 
 int ovh_weight_download(const OvhWeight* w, int8_t* q_nk, float* scale, void* stream) {
   if (!w || !q_nk || !scale) return fail(OV_ERR_INVALID_ARG, "null argument");
+  if (w->f32) return fail(OV_ERR_INVALID_ARG, "weight_download: the weight is fp32");
   const hipStream_t st = as_stream(stream);
   hipError_t e = ovh::launch_weight_to_nk(w->w, q_nk, st);
   if (e == hipSuccess)

@@ -45,6 +45,43 @@ struct GemmArgs {
   int h_tiled = 0;  // hq tile-major (act_index)
 };
 
+// fp32 linear on the f16 matrix cores (gemm_f32.hip).  Weight: hi/lo f16
+// planes of W * 2^-e_n ([Np/32][Ks] fragments of 1 KiB, Np a multiple of 128,
+// Ks = ceil(K / 16)) and the column scales 2^e_n [Np] (0 past N).
+struct F32Weight {
+  int64_t N = 0, K = 0, Np = 0, Ks = 0;
+  _Float16* hi = nullptr;
+  _Float16* lo = nullptr;
+  float* scale = nullptr;
+};
+
+struct GemmF32Args {
+  int M = 0, N = 0;
+  int64_t Ks = 0;
+  const _Float16* ahi = nullptr;  // activation planes, rows padded to 128
+  const _Float16* alo = nullptr;
+  const float* ascale = nullptr;  // [M] row scales 2^e_m
+  const _Float16* whi = nullptr;
+  const _Float16* wlo = nullptr;
+  const float* wscale = nullptr;  // [Np]
+  float* C = nullptr;
+  int64_t ldc = 0;
+  int accumulate = 0;
+};
+
+// halves of one plane for `rows` rows (padded to 128) and K (padded to 16)
+int64_t f32_plane_halves(int64_t rows, int64_t K);
+hipError_t launch_f32_weight(int64_t N, int64_t K, const float* src, int layout, F32Weight& w,
+                             hipStream_t st);
+hipError_t launch_f32_split(int64_t M, int64_t K, const float* A, int64_t Ks, _Float16* hi,
+                            _Float16* lo, float* scale, hipStream_t st);
+// RMSNorm (the reference's rmsnorm_f32 bits) of rows of `cols` = 256 P <= 1024
+// columns, split into activation planes with Ks = cols / 16.
+hipError_t launch_rmsnorm_split(int64_t rows, int64_t cols, const float* x, const float* w,
+                                float eps, int64_t Ks, _Float16* hi, _Float16* lo, float* scale,
+                                hipStream_t st);
+hipError_t launch_gemm_f32(const GemmF32Args& a, hipStream_t st);
+
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
                                 const float* scale_src, DeviceWeight& dst, hipStream_t st);

@@ -47,22 +47,6 @@ __device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
 
-// Workgroup id -> (n tile, m tile), XCD-aware.  Workgroups are dispatched to the
-// 8 XCDs round-robin (id % 8).  The n tiles are split into 8 contiguous ranges of
-// `per` tiles (padded: the grid has 8*per*m_tiles workgroups and those landing on
-// a padding tile return at once); XCD x walks its range m-tile by m-tile, so the
-// weight rows an XCD reads stay in its own L2.
-__device__ __forceinline__ bool tile_of(int id, int n_tiles, int& nt, int& mt) {
-  const int per = (n_tiles + 7) >> 3;
-  const int xcd = id & 7, slot = id >> 3;
-  nt = xcd * per + slot % per;
-  mt = slot / per;
-  return nt < n_tiles;
-}
-
-__host__ __device__ inline int64_t grid_size(int64_t n_tiles, int64_t m_tiles) {
-  return 8 * ((n_tiles + 7) / 8) * m_tiles;
-}
 
 // SB = blocks (32 k each) per LDS stage; the host only launches SB with
 // Kb % SB == 0, so the loop below has no K tail and no predicated loads (which
@@ -326,21 +310,12 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
 // (weights, tile-major codes) the bytes 512 h + 8 l, so each 16 lanes read 128
 // contiguous bytes; in the row-chunk order of row-major codes chunk
 // (l/32)*32 + row, byte 8*((l/16) & 1) (two rows 8 apart share a bank there).
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ i32x4 mfma16_i8(int64_t a, int64_t b) {
   const i32x4 z = {0, 0, 0, 0};
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone): this
-// wavefront's DMA ops older than the last N have landed in LDS and its own LDS
-// reads have returned.
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
 
 // NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.  PIPE:
 // the stage loop runs as a software pipeline (below); without it each stage

@@ -314,6 +314,8 @@ struct OvhLm {
     float* kn = nullptr;
   };
   std::vector<Layer> layers;
+  // the audio head: int8 (nk / kn), or fp32 [K, N] as the reference's default
+  // int8 checkpoint keeps it (f32 planes, see ovh_linear_f32)
   OvhWeight* head = nullptr;
   float* final_norm = nullptr;
   ovh::EmbTable tok{}, aud{};
@@ -435,6 +437,24 @@ int load_linear(const OvhLm& L, const TensorIndex& ix, const std::string& name, 
   return ovh_weight_upload(N, K, static_cast<const int8_t*>(t->data), t->scales, layout, L.st, out);
 }
 
+// The audio head (make_linear, mat.cpp:69-106, as LM's constructor loads it):
+// int8 with per-channel scales in either layout, or fp32 stored pre-transposed
+// [K, N] (the reference's fp32 encoding; an fp32 [N, K] tensor is an error
+// there too).
+int load_head(const OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t N,
+              int64_t K, OvhWeight** out) {
+  const OvhTensorView* t = ix.find(name);
+  if (!t) return missing(name);
+  if (t->ndim != 2 || t->dtype != 0) return load_linear(L, ix, name, N, K, out);
+  if (!t->transposed)
+    return set_error(OV_ERR_INVALID_ARG,
+                     name + ": expected a pre-transposed weight or an int8 [N,K] weight");
+  if (t->dims[0] != K || t->dims[1] != N || !t->data)
+    return set_error(OV_ERR_INVALID_ARG, name + ": shape mismatch (expected [K=" +
+                                             std::to_string(K) + ", N=" + std::to_string(N) + "])");
+  return ovh::weight_upload_f32(N, K, static_cast<const float*>(t->data), 1, L.st, out);
+}
+
 // Embedding table [rows, H]: fp32, or int8 + per-row scale (make_emb, mat.cpp:108-128).
 int load_emb(OvhLm& L, const TensorIndex& ix, const std::string& name, int64_t H,
              ovh::EmbTable* tab, int64_t* rows) {
@@ -470,7 +490,10 @@ int build(OvhLm& L, const TensorIndex& ix) {
   if (rc != OV_OK) return rc;
   if (L.aud_rows != (int64_t)c.n_codebooks * c.audio_vocab)
     return set_error(OV_ERR_INVALID_ARG, "audio embedding rows mismatch");
-  rc = load_linear(L, ix, "audio_heads.weight", (int64_t)c.n_codebooks * c.audio_vocab, H, &L.head);
+  rc = load_head(L, ix, "audio_heads.weight", (int64_t)c.n_codebooks * c.audio_vocab, H, &L.head);
+  if (rc == OV_OK && L.head->f32 && (H % 256 != 0 || H > 1024))
+    rc = set_error(OV_ERR_NOT_IMPLEMENTED,
+                   "an fp32 audio head needs hidden a multiple of 256, at most 1024");
   if (rc == OV_OK) rc = load_norm(L, ix, "llm.norm.weight", H, &L.final_norm);
   if (rc != OV_OK) return rc;
   const OvhTensorView* offs = ix.find("codebook_layer_offsets");
@@ -655,6 +678,11 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
             b_g = take(sizeof(float) * (size_t)(Tpad * I)),  // also the SiLU codes, Tpad rows
             b_u = take(sizeof(float) * (size_t)(T * I)),
             b_lg = take(sizeof(float) * (size_t)(T * CV));
+  // fp32 head: the final norm's output as f16 hi/lo planes and row scales
+  const bool head_f32 = L.head->f32;
+  const size_t hplane = head_f32 ? sizeof(_Float16) * (size_t)ovh::f32_plane_halves(T, H) : 0;
+  const Buf b_hh = take(hplane), b_hl = take(hplane),
+            b_hs = take(head_f32 ? sizeof(float) * (size_t)Tpad : 0);
   // split-f16 attention planes (K and V tile-major, segments padded to 32 keys)
   int64_t vt_cols = 0;
   std::vector<int64_t> vt_off(segs.size());
@@ -835,6 +863,29 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
         if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
       }
+    }
+    if (head_f32) {
+      // rmsnorm_f32 then Mat's fp32 product (lm.cpp:383-385)
+      const ovh::F32Weight& fw = L.head->fw;
+      ovh::GemmF32Args ha;
+      ha.M = (int)T;
+      ha.N = (int)fw.N;
+      ha.Ks = fw.Ks;
+      ha.ahi = static_cast<_Float16*>(at(b_hh));
+      ha.alo = static_cast<_Float16*>(at(b_hl));
+      ha.ascale = static_cast<float*>(at(b_hs));
+      ha.whi = fw.hi;
+      ha.wlo = fw.lo;
+      ha.wscale = fw.scale;
+      ha.C = logits;
+      ha.ldc = CV;
+      OVH_HIP(ovh::launch_rmsnorm_split(T, H, x, L.final_norm, c.rms_eps, fw.Ks,
+                                        static_cast<_Float16*>(at(b_hh)),
+                                        static_cast<_Float16*>(at(b_hl)),
+                                        static_cast<float*>(at(b_hs)), st),
+              "final norm (split) launch");
+      OVH_HIP(ovh::launch_gemm_f32(ha, st), "fp32 head launch");
+      return OV_OK;
     }
     if ((rc = norm_q(L.final_norm)) != OV_OK)
       return rc;

@@ -98,4 +98,33 @@ __device__ __forceinline__ float silu_up_lane(float g, float u) {
   return __fmul_rn(__fdiv_rn(g, d), u);
 }
 
+// Workgroup id -> (n tile, m tile), XCD-aware.  Workgroups are dispatched to the
+// 8 XCDs round-robin (id % 8).  The n tiles are split into 8 contiguous ranges of
+// `per` tiles (padded: the grid has 8*per*m_tiles workgroups and those landing on
+// a padding tile return at once); XCD x walks its range m-tile by m-tile, so the
+// weight rows an XCD reads stay in its own L2.
+__device__ __forceinline__ bool tile_of(int id, int n_tiles, int& nt, int& mt) {
+  const int per = (n_tiles + 7) >> 3;
+  const int xcd = id & 7, slot = id >> 3;
+  nt = xcd * per + slot % per;
+  mt = slot / per;
+  return nt < n_tiles;
+}
+
+__host__ __device__ inline int64_t grid_size(int64_t n_tiles, int64_t m_tiles) {
+  return 8 * ((n_tiles + 7) / 8) * m_tiles;
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone): this
+// wavefront's DMA ops older than the last N have landed in LDS and its own LDS
+// reads have returned.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// LDS destination of global_load_lds (address space 3).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
 }  // namespace ovh

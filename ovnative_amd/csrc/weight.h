@@ -11,6 +11,10 @@ struct OvhWeight {
   // rows interleaved gate/up in 16-row groups (weight_interleave16): only the
   // SiLU-fused operator takes such a weight
   bool silu_pair = false;
+  // an fp32 weight (ovh_weight_upload_f32): f16 planes in fw, w unused except
+  // for N and K; only ovh_linear_f32 takes it
+  bool f32 = false;
+  ovh::F32Weight fw;
 };
 
 namespace ovh {
@@ -26,4 +30,7 @@ int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, 
 int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                     const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
                     bool a_tiled);
+// fp32 weight from host memory, OVW1 layout 0 ([N,K]) or 1 ([K,N])
+int weight_upload_f32(int64_t N, int64_t K, const float* w, int layout, hipStream_t st,
+                      OvhWeight** out);
 }  // namespace ovh

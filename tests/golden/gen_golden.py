@@ -133,6 +133,17 @@ def main() -> None:
             out[f"attn{i}_{name}"] = arr
         out[f"attn{i}_masked"] = np.array(int(masked), np.int64)
 
+    # -- linear_f32_ld (gemm.cpp:884-905): Mat's fp32 branch, W [K, N] ---------
+    # (the fp32 audio head of the default int8 checkpoint); N % 8 tails included
+    fcases = [(3, 16, 24), (9, 40, 100), (8, 69, 33), (2, 136, 64), (17, 7, 1024)]
+    for i, (M, N, K) in enumerate(fcases):
+        A = act(rng, M, K, scale=rng.uniform(0.5, 3.0))
+        W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+        Cin = rng.standard_normal((M, N)).astype(np.float32)
+        out[f"lf32{i}_A"], out[f"lf32{i}_W"], out[f"lf32{i}_Cin"] = A, W, Cin
+        out[f"lf32{i}_C"] = ref.linear_f32(A, W)
+        out[f"lf32{i}_Cadd"] = ref.linear_f32(A, W, Cin, accumulate=True)
+
     path = os.path.join(HERE, "int8nk_golden.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path)} bytes")

@@ -19,8 +19,11 @@ FULL1 = dict(n_layers=1, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, in
 FULL28 = dict(FULL1, n_layers=28)
 
 
-def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True):
-    """Returns (tensors for ovw1.write / views, {name: (array, scales, transposed)})."""
+def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True,
+            head_fp32: bool = False):
+    """Returns (tensors for ovw1.write / views, {name: (array, scales, transposed)}).
+    head_fp32: the audio head stays fp32, stored [K, N], as the reference's
+    default int8 checkpoint keeps it (tools/convert_weights.py --int8-keep)."""
     rng = np.random.default_rng(seed)
     H, NH, NKV, D, I = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["inter"]
     Cb, V = cfg["n_codebooks"], cfg["audio_vocab"]
@@ -43,7 +46,11 @@ def make_lm(seed: int, cfg: dict, layout: str = "nk", emb_int8: bool = True):
 
     emb("llm.embed_tokens.weight", cfg["vocab"])
     emb("audio_embeddings.weight", Cb * V)
-    lin("audio_heads.weight", Cb * V, H)
+    if head_fp32:
+        w = (rng.standard_normal((Cb * V, H)) * 0.02).astype(np.float32)
+        ts.append(ovw1.Tensor("audio_heads.weight", np.ascontiguousarray(w.T), 1))
+    else:
+        lin("audio_heads.weight", Cb * V, H)
     norm("llm.norm.weight", H)
     ts.append(ovw1.Tensor("codebook_layer_offsets", np.arange(Cb, dtype=np.int64) * V))
     for i in range(cfg["n_layers"]):

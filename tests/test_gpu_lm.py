@@ -517,3 +517,62 @@ def test_config4_generate_32_steps(full_lm):
                                seed=1234)
     assert np.all(got != V - 1)
     assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# The reference's default int8 checkpoint: audio head kept fp32 [K, N]
+# (tools/convert_weights.py --int8-keep audio_heads; lm.cpp:383-385)
+
+@pytest.mark.parametrize("cfg_name", ["SMALL", "FULL1"])
+def test_fp32_head_forward(oracle, tmp_path, cfg_name):
+    """The runner accepts the fp32 head: its logits equal the oracle's forward
+    with the device attention substituted up to the head's split-f16 products
+    (max |d| <= 2^-17 * max|logit|; everything before the head is bit-exact),
+    and against the compiled reference's own LM::forward on the same OVW1 file
+    they pass the same bars as the int8 head does against the pure oracle."""
+    import ovnative_amd as ov
+    from ovnative_amd import ovw1
+    cfg = dict(SMALL=SMALL, FULL1=FULL1)[cfg_name]
+    ts, table = make_lm(61, cfg, head_fp32=True)
+    ids, am, attn, pos = make_inputs(62, cfg, 2, 96 if cfg_name == "SMALL" else 300, 12)
+    path = str(tmp_path / "lm_fp32head.ovw")
+    ovw1.write(path, ts)
+    lm = ov.LM.from_file(path, _cfg(cfg))
+    try:
+        got = lm.forward(ids, am, attn, pos)
+    finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(cfg, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(cfg))
+    d = float(np.abs(flat.astype(np.float64) - hybrid).max() / np.abs(hybrid).max())
+    print(f"fp32 head ({cfg_name}): max |d| / max|logit| vs the hybrid oracle {d:.3g}")
+    assert d <= 2.0 ** -17
+    import oracle as oracle_mod
+    if not oracle_mod.reference_available():
+        pytest.skip("oracle/_ref (the compiled reference) is not built here")
+    reference = oracle_mod.Reference()
+    if not reference.vnni_available():
+        pytest.skip("the reference's int8-nk VNNI path is not available on this host")
+    h = reference.lm_open(path, cfg)
+    try:
+        ref = reference.lm_forward(h, cfg, ids, am, attn, pos)
+    finally:
+        reference.lm_close(h)
+    ref_flat = ref.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    st = _logit_stats(flat, ref_flat, V)
+    print(f"fp32 head ({cfg_name}) vs the reference's LM::forward: {st}")
+    assert st["max_rel"] <= LOGIT_TOL and st["cos"] >= LOGIT_COS
+
+
+def test_fp32_head_layout_error():
+    """An fp32 head stored [N, K] is refused, as the reference's make_linear does."""
+    import ovnative_amd as ov
+    from ovnative_amd import ovw1
+    ts, _ = make_lm(63, dict(SMALL, n_layers=1), head_fp32=True)
+    ts = [ovw1.Tensor(t.name, np.ascontiguousarray(t.array.T), 0) if t.name == "audio_heads.weight"
+          else t for t in ts]
+    with pytest.raises(ov.InvalidArgument):
+        ov.LM.from_tensors(ts, _cfg(dict(SMALL, n_layers=1)))

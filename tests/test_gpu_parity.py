@@ -516,3 +516,74 @@ def test_silu_gate_linear_small_width_and_errors(oracle):
     with pytest.raises(ov.OvhError) as e:
         ov.silu_gate_linear(aq96, asc96, g96)
     assert e.value.code == ov.OV_ERR_NOT_IMPLEMENTED
+
+
+# ---------------------------------------------------------------------------
+# Mat's fp32 branch (the fp32 audio head): split-f16 matrix-core products
+
+# |gpu - reference| <= F32_TOL * sum_k |A[m,k] W[k,n]| per output: the split
+# keeps ~22 bits of each operand (hi + lo; lo*lo dropped, ~2^-22 relative per
+# product) and both sides sum in fp32 in different orders.
+F32_TOL = 2.0 ** -18
+
+
+def _check_f32(got, want, A, W):
+    bound = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64))
+    err = np.abs(got.astype(np.float64) - want)
+    ratio = float((err / np.maximum(bound, 1e-30)).max())
+    rel = float(err.max() / max(np.abs(want).max(), 1e-30))
+    print(f"linear_f32 {A.shape} x {W.shape}: max |d| / sum|aw| = {ratio:.3g}, "
+          f"max |d| / max|ref| = {rel:.3g}")
+    assert ratio <= F32_TOL
+    assert rel <= 1e-3   # the north star's fp32 bar
+
+
+@pytest.mark.parametrize("M,N,K", [(600, 8200, 1024), (37, 69, 100), (1, 64, 16), (130, 136, 33),
+                                   (256, 1024, 3072)])
+def test_linear_f32_vs_oracle(oracle, M, N, K):
+    """ovh_linear_f32 against the oracle's linear_f32_ld (the reference's fma chain,
+    pinned bit for bit to the compiled reference): store and accumulate, weights
+    uploaded in both OVW1 layouts; (600, 8200, 1024) is the fp32 audio head at
+    BASELINE config 4."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(M + N + K)
+    A = (rng.standard_normal((M, K)) * rng.uniform(0.5, 4)).astype(np.float32)
+    A[:, rng.integers(0, K, 3)] *= 20
+    W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    want = oracle.linear_f32(A, W)
+    w_kn = ov.Weight.from_host_f32(W, layout=1)
+    got = host(ov.linear_f32(dev(A), w_kn))
+    _check_f32(got, want, A, W)
+    w_nk = ov.Weight.from_host_f32(np.ascontiguousarray(W.T), layout=0)
+    assert np.array_equal(bits(host(ov.linear_f32(dev(A), w_nk))), bits(got))
+    Cin = rng.standard_normal((M, N)).astype(np.float32)
+    c = dev(Cin)
+    ov.linear_f32(dev(A), w_kn, c, accumulate=True)
+    assert np.array_equal(bits(host(c)), bits((Cin + got).astype(np.float32)))
+
+
+def test_linear_f32_ranges_and_errors(oracle):
+    """Power-of-two row and column scales keep tiny and huge operands in f16's
+    range (values near 1e-30 and 1e30 in different rows/columns), an all-zero row
+    gives zeros, and the int8 operators refuse an fp32 weight (and back)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(3)
+    M, N, K = 6, 40, 64
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    A[1] *= 1e-30
+    A[2] *= 1e30
+    A[3] = 0
+    W = rng.standard_normal((K, N)).astype(np.float32)
+    W[:, 5] *= 1e-25
+    W[:, 6] *= 1e-10
+    want = oracle.linear_f32(A, W)
+    w = ov.Weight.from_host_f32(W)
+    got = host(ov.linear_f32(dev(A), w))
+    assert np.all(got[3] == 0)
+    _check_f32(got, want, A, W)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    with pytest.raises(ov.InvalidArgument):
+        ov.linear_q(aq, asc, w)
+    q, s = oracle.quantize_weight_rows(rng.standard_normal((N, K)).astype(np.float32))
+    with pytest.raises(ov.InvalidArgument):
+        ov.linear_f32(dev(A), ov.Weight.from_host(q, s))

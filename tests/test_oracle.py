@@ -243,6 +243,11 @@ def test_fused_equals_unfused(oracle):
 def golden_mismatches(o, golden):
     """Names of the golden checks that oracle `o` fails."""
     bad = []
+    for c in _cases(golden, "lf32"):
+        A, W, Cin = golden[c + "_A"], golden[c + "_W"], golden[c + "_Cin"]
+        if not (np.array_equal(bits(o.linear_f32(A, W)), bits(golden[c + "_C"])) and
+                np.array_equal(bits(o.linear_f32(A, W, Cin, True)), bits(golden[c + "_Cadd"]))):
+            bad.append(c)
     for c in _cases(golden, "quant"):
         aq, asc = o.quantize(golden[c + "_A"])
         if not (np.array_equal(aq, golden[c + "_aq"]) and
@@ -298,7 +303,7 @@ def test_weight_scale_floor(oracle):
     assert np.all(s == np.float32(1e-12)) and np.all(q == 0)
 
 
-@pytest.mark.parametrize("plant", [1, 2, 3, 4, 5, 7, 8, 9])
+@pytest.mark.parametrize("plant", [1, 2, 3, 4, 5, 7, 8, 9, 10])
 def test_planted_mistakes_are_caught(golden, plant, tmp_path):
     """Rebuild the oracle with one deliberate, plausible mistake (OVO_PLANT in
     oracle/ovoracle.c) and check that the golden vectors reject it."""
@@ -309,3 +314,25 @@ def test_planted_mistakes_are_caught(golden, plant, tmp_path):
                     f"-DOVO_PLANT={plant}", "-o", str(lib), f"{HERE}/ovoracle.c", "-lm"],
                    check=True)
     assert golden_mismatches(Oracle(str(lib)), golden) != []
+
+
+def test_linear_f32_closed_form_and_reference(oracle, reference):
+    """linear_f32 (Mat's fp32 branch): integer-valued operands with sums below
+    2^24 give the exact integer product whatever the order; a K = 1 product is
+    one correctly rounded multiply; and on random data the oracle's fma chain is
+    the compiled reference's linear_f32_ld bit for bit (N % 8 tails included)."""
+    rng = np.random.default_rng(31)
+    A = rng.integers(-50, 51, (13, 70)).astype(np.float32)
+    W = rng.integers(-50, 51, (70, 29)).astype(np.float32)
+    exact = A.astype(np.int64) @ W.astype(np.int64)
+    assert np.array_equal(oracle.linear_f32(A, W), exact.astype(np.float32))
+    a1 = rng.standard_normal((5, 1)).astype(np.float32)
+    w1 = rng.standard_normal((1, 11)).astype(np.float32)
+    assert np.array_equal(bits(oracle.linear_f32(a1, w1)), bits((a1 * w1).astype(np.float32)))
+    for M, N, K in ((7, 8200 // 40, 1024), (3, 13, 5), (40, 64, 300)):
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+        Cin = rng.standard_normal((M, N)).astype(np.float32)
+        assert np.array_equal(bits(oracle.linear_f32(A, W)), bits(reference.linear_f32(A, W)))
+        assert np.array_equal(bits(oracle.linear_f32(A, W, Cin, True)),
+                              bits(reference.linear_f32(A, W, Cin, True)))

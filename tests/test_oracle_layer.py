@@ -217,20 +217,24 @@ def test_guided_sample_host_alias_quirk(oracle):
     assert not np.allclose(s_dev, s_cpu)
 
 
-@pytest.mark.parametrize("layout,batch,seq,text", [("nk", 2, 40, 8), ("nk", 1, 17, 5),
-                                                   ("kn", 2, 24, 6)])
-def test_lm_forward_against_reference(reference, oracle, tmp_path, layout, batch, seq, text):
+@pytest.mark.parametrize("layout,batch,seq,text,head_fp32", [
+    ("nk", 2, 40, 8, False), ("nk", 1, 17, 5, False), ("kn", 2, 24, 6, False),
+    ("nk", 2, 30, 6, True)], ids=["nk-b2", "nk-b1", "kn-b2", "nk-b2-fp32head"])
+def test_lm_forward_against_reference(reference, oracle, tmp_path, layout, batch, seq, text,
+                                      head_fp32):
     """The oracle's forward (composition of the restated pieces) is bit-identical to
     the reference's LM::forward (lm.cpp, compiled from source) on an OVW1 file
     written by ovnative_amd/ovw1.py.  For kn checkpoints the reference CPU takes
     its non-VNNI fp32-activation kernel (mat.cpp:82-90, no activation
     quantisation), a different arithmetic; the HIP path computes int8-nk numerics
-    for both layouts, so kn is only checked to stay close (cosine >= 0.9999)."""
+    for both layouts, so kn is only checked to stay close (cosine >= 0.9999).
+    fp32head: the audio head fp32 [K, N], as the reference's default int8
+    checkpoint keeps it (final rmsnorm_f32, then Mat's fp32 branch)."""
     from lm_fixture import SMALL, make_inputs, make_lm
     from ovnative_amd import ovw1
     if not reference.vnni_available():
         pytest.skip("the reference's int8-nk VNNI path is not available on this host")
-    ts, table = make_lm(5, SMALL, layout=layout)
+    ts, table = make_lm(5, SMALL, layout=layout, head_fp32=head_fp32)
     path = str(tmp_path / "lm.ovw")
     ovw1.write(path, ts)
     ids, am, attn, pos = make_inputs(6, SMALL, batch, seq, text)
