@@ -1,6 +1,9 @@
 """The CFG decoding loop (ovh_lm_generate, tts.cpp:165-364): the restated host
 logic is pinned here on the CPU; tests/test_gpu_lm.py runs the device loop
 against it."""
+import math
+from fractions import Fraction
+
 import numpy as np
 
 import oracle
@@ -55,3 +58,36 @@ def test_run_sampling_logic_with_a_stub_model():
     done = [(c[0][:, S - T:] != V - 1).sum() for c in calls]
     assert done == list(np.cumsum([0] + sched[:-1]))
     assert np.array_equal(calls[-1][1][:, :T], calls[-1][0][:, S - T:])
+
+
+# tts.cpp:231-249 at the reference's defaults (32 steps, t_shift 0.1f, 8 codebooks x
+# 260 frames).  By hand, step 0: ts_1 = 0.1 * (1/32) / (1 - 0.9/32) = 1/311, and
+# ceil(2080/311) = ceil(6.688) = 7.
+DEFAULT_SCHEDULE = [7, 8, 8, 8, 9, 10, 10, 11, 12, 13, 14, 15, 16, 17, 19, 21, 23, 26, 29, 32,
+                    37, 42, 49, 57, 68, 82, 101, 128, 166, 226, 325, 491]
+
+
+def _exact_schedule(steps, t_shift, total):
+    """The schedule in exact rational arithmetic (t_shift as the float32 value the
+    option holds): ts_i = a t / (1 + (a - 1) t), t = i / steps; per step
+    ceil(total (ts_{s+1} - ts_s)) capped by what remains, the last step the rest."""
+    a = Fraction(float(np.float32(t_shift)))
+    ts = [a * Fraction(i, steps) / (1 + (a - 1) * Fraction(i, steps)) for i in range(steps + 1)]
+    out, rem = [], total
+    for s in range(steps):
+        num = rem if s == steps - 1 else min(math.ceil(total * (ts[s + 1] - ts[s])), rem)
+        out.append(num)
+        rem -= num
+    return out
+
+
+def test_schedule_known_answer():
+    """The restated schedule (double arithmetic, as tts.cpp) equals the known
+    answer at the defaults, which the exact-rational closed form reproduces; a
+    floor in place of the ceil, or i/steps in place of the shifted grid, would
+    not (they change the per-step counts even where the sums agree)."""
+    assert sum(DEFAULT_SCHEDULE) == 2080
+    assert _exact_schedule(32, 0.1, 2080) == DEFAULT_SCHEDULE
+    assert oracle.cfg_schedule(32, 0.1, 2080) == DEFAULT_SCHEDULE
+    for steps, shift, total in [(8, 0.1, 96), (16, 0.5, 1000), (32, 0.1, 8 * 75), (4, 2.0, 33)]:
+        assert oracle.cfg_schedule(steps, shift, total) == _exact_schedule(steps, shift, total)

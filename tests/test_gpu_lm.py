@@ -576,3 +576,49 @@ def test_fp32_head_layout_error():
           else t for t in ts]
     with pytest.raises(ov.InvalidArgument):
         ov.LM.from_tensors(ts, _cfg(dict(SMALL, n_layers=1)))
+
+
+def test_device_sampling_invariants(small_lm):
+    """The device sampler keeps what tts.cpp:296-326 fixes independently of
+    rounding: uncond == cond makes g = 2 pick what g = 0 picks; a constant added
+    to one (codebook, frame) row of either plane changes nothing beyond
+    rounding; the layer penalty only subtracts c * penalty; the mask token (the
+    last id) is never chosen, even as the largest logit."""
+    ts, table, lm = small_lm
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    S, T = 20, 12
+    rng = np.random.default_rng(45)
+    cond = (rng.standard_normal((S, Cb * V)) * 2).astype(np.float32)
+    uncond = (rng.standard_normal((T, Cb * V)) * 2).astype(np.float32)
+    cond[S - T + 3, 4 * V + V - 1] = 50.0
+    uncond[3, 4 * V + V - 1] = 50.0
+
+    def run(c, u, g, pen):
+        dc, du = torch.from_numpy(c).cuda(), torch.from_numpy(np.ascontiguousarray(u)).cuda()
+        torch.cuda.synchronize()
+        return lm.sample(dc.data_ptr(), S, du.data_ptr(), u.shape[0], T, g, pen)
+
+    p0, s0 = run(cond, cond[S - T:], 0.0, 5.0)
+    p2, s2 = run(cond, cond[S - T:], 2.0, 5.0)
+    assert np.array_equal(p0, p2)
+    np.testing.assert_allclose(s2, s0, rtol=0, atol=4e-6)
+    bp, bs = run(cond, uncond, 2.0, 5.0)
+    c2, u2 = cond.copy(), uncond.copy()
+    c2[S - T + 1, 2 * V:3 * V] += 3.0
+    u2[4, 5 * V:6 * V] -= 7.0
+    sp, ss = run(c2, u2, 2.0, 5.0)
+    # near-ties aside (top-two gap of the float64 guided values)
+    lc = cond[S - T:].reshape(T, Cb, V).astype(np.float64)
+    lu = uncond.reshape(T, Cb, V).astype(np.float64)
+    lsm = lambda x: x - (np.log(np.exp(x - x.max(-1, keepdims=True)).sum(-1, keepdims=True)) +
+                         x.max(-1, keepdims=True))
+    mix = lsm(lsm(lc) + 2.0 * (lsm(lc) - lsm(lu)))
+    mix[..., V - 1] = -np.inf
+    top = np.sort(mix, axis=-1)[..., -2:]
+    clear = (top[..., 1] - top[..., 0] > 1e-4).T
+    assert np.array_equal(sp[clear], bp[clear])
+    np.testing.assert_allclose(ss, bs, rtol=0, atol=2e-5)
+    np_, ns = run(cond, uncond, 2.0, 0.0)
+    assert np.array_equal(np_, bp)
+    np.testing.assert_allclose(ns - 5.0 * np.arange(Cb)[:, None], bs, rtol=0, atol=8e-6)
+    assert np.all(bp != V - 1) and np.all(p0 != V - 1)

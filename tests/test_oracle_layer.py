@@ -198,6 +198,39 @@ def test_guided_sample_properties(oracle, g):
     np.testing.assert_allclose(score, wscore, rtol=0, atol=2e-5)
 
 
+def test_guided_sample_invariants(oracle):
+    """What tts.cpp:296-326 fixes independently of rounding: (1) with the
+    unconditional logits equal to the conditional ones the guidance term
+    vanishes, so g = 2 picks what g = 0 picks, with the same score up to the
+    second log_softmax's rounding; (2) log_softmax removes a constant added to
+    one (codebook, frame) row of either plane; (3) the layer penalty only
+    subtracts c * penalty from codebook c's scores; (4) the mask token (the last
+    id) is never chosen, even as the largest logit."""
+    rng = np.random.default_rng(44)
+    C, V, S, T = 8, 1025, 10, 6
+    cond = (rng.standard_normal((S, C * V)) * 2).astype(np.float32)
+    uncond = (rng.standard_normal((T, C * V)) * 2).astype(np.float32)
+    cond[S - T + 2, 3 * V + V - 1] = 50.0
+    uncond[2, 3 * V + V - 1] = 50.0
+    p0, s0 = oracle.guided_sample(cond, S, cond[S - T:], C, V, T, 0.0, 5.0)
+    p2, s2 = oracle.guided_sample(cond, S, cond[S - T:], C, V, T, 2.0, 5.0)
+    assert np.array_equal(p0, p2)
+    np.testing.assert_allclose(s2, s0, rtol=0, atol=4e-6)
+    base_p, base_s = oracle.guided_sample(cond, S, uncond, C, V, T, 2.0, 5.0)
+    _, _, gap = _np_guided(cond, S, uncond, C, V, T, 2.0, 5.0, V - 1)
+    clear = gap > 1e-4
+    c2, u2 = cond.copy(), uncond.copy()
+    c2[S - T + 1, 2 * V:3 * V] += 3.0       # (codebook 2, frame 1) of the cond plane
+    u2[4, 5 * V:6 * V] -= 7.0               # (codebook 5, frame 4) of the uncond plane
+    sh_p, sh_s = oracle.guided_sample(c2, S, u2, C, V, T, 2.0, 5.0)
+    assert np.array_equal(sh_p[clear], base_p[clear])
+    np.testing.assert_allclose(sh_s, base_s, rtol=0, atol=2e-5)
+    np_p, np_s = oracle.guided_sample(cond, S, uncond, C, V, T, 2.0, 0.0)
+    assert np.array_equal(np_p, base_p)
+    np.testing.assert_allclose(np_s - 5.0 * np.arange(C)[:, None], base_s, rtol=0, atol=8e-6)
+    assert np.all(base_p != V - 1) and np.all(p0 != V - 1)
+
+
 def test_guided_sample_host_alias_quirk(oracle):
     """tts.cpp's host path renormalises lp_mix with log_softmax(x, n, x) in place,
     so its guided values are exp(mix - m) - lse (the function's last loop reads
