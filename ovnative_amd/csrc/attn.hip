@@ -5,6 +5,7 @@
 
 #include "attn.h"
 #include "ovh_common.h"
+#include "qk_common.h"
 
 namespace ovh {
 
@@ -318,13 +319,6 @@ hipError_t launch_attention(const AttnArgs& args, int max_rows, hipStream_t st) 
 // structure otherwise.  Values beyond the f16 range would become inf: the split
 // pass reports them through `overflow` (the reference's own GPU path runs its
 // activations in fp16 too, cuda_lm.cu:1086-1160).
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void split16(float x, _Float16& hi, _Float16& lo) {
-  hi = (_Float16)x;
-  lo = (_Float16)(x - (float)hi);
-}
 
 __device__ __forceinline__ f32x16 mfma_h(h8 a, h8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -334,12 +328,6 @@ __device__ __forceinline__ f32x16 mfma_h(h8 a, h8 b, f32x16 c) {
 // Tile-major (see AttnSplit): per (KV head, 32-key block) 8 fragments of 64
 // lanes x 8 halves, each the 16 bytes one lane reads for one matrix-core
 // operand, so a wavefront's fragment load is 1 KiB of contiguous memory.
-constexpr int kTileHalves = 8 * 64 * 8;  // per (KV head, key block) and plane
-
-// K: key kk of block kb, dim d -> fragment d/16, lane kk + 32*((d/8)%2), half d%8.
-__device__ __forceinline__ int64_t k_tile_index(int kvh, int64_t nkb, int64_t kb, int kk, int d) {
-  return ((((int64_t)kvh * nkb + kb) * 8 + (d >> 4)) * 64 + kk + 32 * ((d >> 3) & 1)) * 8 + (d & 7);
-}
 
 // V (and K) of one 32-key x 32-dim tile (key tile `kt` of segment `s`, dims
 // 32*dq..+31 of KV head `kvh`).  V goes through LDS: head-dim row 32j + r holds
@@ -428,35 +416,6 @@ __device__ __forceinline__ bool split_v_job(const AttnArgs& a, const AttnSplit& 
 __global__ __launch_bounds__(256) void split_kv_kernel(AttnArgs a, AttnSplit sp, int ktiles) {
   __shared__ float tile[32][33];
   if (split_v_job(a, sp, (int64_t)blockIdx.x, ktiles, tile, true)) atomicOr(sp.overflow, 1u);
-}
-
-// The same RMSNorm + RoPE with 8 lanes per head vector: lane j of the group
-// holds x[j + 8i], i = 0..15 (D = 128), i.e. the reference's fma chain j, and
-// both members of the rotation pairs (j + 8i, j + 8i + 64), i < 8.  The chain
-// runs in registers, the 8 chain sums are added left to right after 7 lane
-// reads, and every value is the one norm_rope_pair computes.
-__device__ __forceinline__ void norm_rope_lanes8(float (&x)[16], const float* __restrict__ w,
-                                                 const float* __restrict__ cos_row,
-                                                 const float* __restrict__ sin_row, float eps,
-                                                 int j) {
-  constexpr int D = kAttnD, half = D / 2;
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s = fmaf(x[i], x[i], s);
-  const int g0 = (threadIdx.x & 63) & ~7;  // the group's first lane
-  float sum = __shfl(s, g0);
-#pragma unroll
-  for (int c = 1; c < 8; ++c) sum = __fadd_rn(sum, __shfl(s, g0 + c));
-  const float scale = __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)D), eps)));
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int d = j + 8 * i;
-    const float c = cos_row[d], sn = sin_row[d];
-    const float na = __fmul_rn(__fmul_rn(x[i], scale), w[d]);
-    const float nb = __fmul_rn(__fmul_rn(x[i + 8], scale), w[d + half]);
-    x[i] = fmaf(na, c, -__fmul_rn(nb, sn));
-    x[i + 8] = fmaf(na, sn, __fmul_rn(nb, c));
-  }
 }
 
 // The runner's form of qk-norm + RoPE + plane split, in one launch.  The first

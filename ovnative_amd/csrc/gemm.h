@@ -11,7 +11,32 @@ constexpr int kMaxSlices = 8;
 // N-tile the kernels use (32..128 rows) reads in-bounds rows and zero scales.
 constexpr int kRowPad = 128;
 
-enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2, kSiluQuant = 3 };
+enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2, kSiluQuant = 3, kQkvNorm = 4 };
+
+// kQkvNorm: the runner's merged q/k/v GEMM with qk_norm_rope_f32 and the
+// split-f16 attention's K/V planes in its epilogue.  Each 128-column output
+// tile is one head: q heads (columns < QD) are normalised, rotated and stored
+// fp32 to q [rows][QD]; k heads are normalised, rotated and written to the K
+// planes; v heads to the V planes (layouts of AttnSplit, attn.h).  Rows map to
+// the attention segments (row0, rows) whose keys sit at plane key-block
+// offsets vt_off; padding keys of each segment's last block are written as 0.
+constexpr int kQkvMaxSegs = 32;
+struct QkvFuse {
+  int32_t QD = 0, KVD = 0;
+  int32_t n_segs = 0;
+  int32_t row0[kQkvMaxSegs] = {0}, rows[kQkvMaxSegs] = {0};
+  int64_t vt_off[kQkvMaxSegs] = {0};
+  int64_t nkb = 0;                      // key blocks per KV head in a plane (vt_cols / 32)
+  const float* cos_tab = nullptr;       // RoPE tables [rows][64]
+  const float* sin_tab = nullptr;
+  float eps = 0.f;
+  float* q = nullptr;                   // normalised, rotated q [rows][QD]
+  _Float16* kh = nullptr;
+  _Float16* kl = nullptr;
+  _Float16* vh = nullptr;
+  _Float16* vl = nullptr;
+  uint32_t* overflow = nullptr;         // set when a k or v value is beyond f16
+};
 
 // Device weight: int8 [Npad][Kp] row-major (row n = output channel n, K tail
 // and rows >= N zero) and fp32 scale [Npad] (0 beyond N).
@@ -43,6 +68,10 @@ struct GemmArgs {
   float* hsc = nullptr;
   int64_t hKp = 0;
   int h_tiled = 0;  // hq tile-major (act_index)
+  // kQkvNorm: the layout-wide part in device memory, the layer's norm weights
+  const QkvFuse* qf = nullptr;
+  const float* qnw = nullptr;
+  const float* knw = nullptr;
 };
 
 // fp32 linear on the f16 matrix cores (gemm_f32.hip).  Weight: hi/lo f16

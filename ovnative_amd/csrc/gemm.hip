@@ -35,6 +35,7 @@
 // contiguous range of weight tiles, so an XCD's L2 holds its own weight slice.
 #include "gemm.h"
 #include "ovh_common.h"
+#include "qk_common.h"
 
 namespace ovh {
 
@@ -570,6 +571,152 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 
   if constexpr (DUMP) return;
 
+  if constexpr (MODE == kQkvNorm) {
+    // One head (128 columns) of 32 rows per workgroup; wavefront wn holds
+    // columns 32 wn .. +31.  The values are those the sliced store would write
+    // (f * wscale); then, as qk_norm_rope_f32 and the plane split do them:
+    // v heads straight to the V planes, q and k heads through LDS (8 lanes per
+    // head vector, norm_rope_lanes8), q stored fp32, k to the K planes.
+    static_assert(BN == 128 && BM == 32 && WM == 1 && NW == 4 && FN == 2 && FM == 2,
+                  "kQkvNorm: 128 x 32 tiles of four wavefronts");
+    const QkvFuse& F = *a.qf;
+    const int QD = F.QD, KVD = F.KVD;
+    float v[FN][FM][4];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + n0 + wn * 32 + i * 16 + 4 * q);
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][j][e] = __fmul_rn(f[i][j][e], ws[e]);
+    }
+    // attention segment of row r (rows of a segment are contiguous) and the
+    // row's key position in it
+    auto seg_of = [&](int64_t r, int& sg, int& p) __attribute__((always_inline)) {
+      for (sg = 0; sg < F.n_segs; ++sg) {
+        const int64_t r0 = F.row0[sg];
+        if (r >= r0 && r < r0 + F.rows[sg]) {
+          p = (int)(r - r0);
+          return true;
+        }
+      }
+      return false;
+    };
+    // keys past the end of each segment whose last row is in this tile, up to
+    // the end of its last 32-key block: zeros in this head's planes
+    auto zero_pad = [&](bool is_v, int kvh) __attribute__((always_inline)) {
+      for (int sg = 0; sg < F.n_segs; ++sg) {
+        const int64_t last = (int64_t)F.row0[sg] + F.rows[sg] - 1;
+        if (F.rows[sg] <= 0 || last < m0 || last >= m0 + BM || last >= a.M) continue;
+        const int p0 = F.rows[sg], p1 = (F.rows[sg] + 31) / 32 * 32;
+        const int per_key = is_v ? kHeadD : kHeadD / 8;
+        for (int t = threadIdx.x; t < (p1 - p0) * per_key; t += 64 * NW) {
+          const int p = p0 + t / per_key, c = t - (t / per_key) * per_key;
+          const int64_t kb = F.vt_off[sg] / 32 + p / 32;
+          if (is_v) {
+            const int64_t at = v_tile_index(kvh, F.nkb, kb, p & 31, c);
+            F.vh[at] = (_Float16)0.f;
+            F.vl[at] = (_Float16)0.f;
+          } else {
+            const int64_t at = k_tile_index(kvh, F.nkb, kb, p & 31, 8 * c);
+            const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            *reinterpret_cast<h8*>(F.kh + at) = z;
+            *reinterpret_cast<h8*>(F.kl + at) = z;
+          }
+        }
+      }
+    };
+    bool bad = false;
+    if (n0 >= QD + KVD) {  // a v head (uniform for the workgroup)
+      const int kvh = (n0 - QD - KVD) / kHeadD;
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int64_t r = m0 + j * 16 + (lane & 15);
+        int sg, p;
+        if (r >= a.M || !seg_of(r, sg, p)) continue;
+        const int64_t kb = F.vt_off[sg] / 32 + p / 32;
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = v[i][j][e];
+            bad |= !(fabsf(x) < 65504.f);
+            _Float16 hi, lo;
+            split16(x, hi, lo);
+            const int64_t at = v_tile_index(kvh, F.nkb, kb, p & 31, wn * 32 + i * 16 + 4 * q + e);
+            F.vh[at] = hi;
+            F.vl[at] = lo;
+          }
+      }
+      zero_pad(true, kvh);
+      if (bad) atomicOr(F.overflow, 1u);
+      return;
+    }
+    // q or k head: the tile through LDS (the ring is free once every wavefront
+    // has left the K loop)
+    __syncthreads();
+    float(*xs)[kHeadD + 4] = reinterpret_cast<float(*)[kHeadD + 4]>(&smem[0][0]);
+    static_assert(BM * (kHeadD + 4) * 4 <= STAGE, "the staged head fits in one ring slot");
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        *reinterpret_cast<f32x4*>(&xs[j * 16 + (lane & 15)][wn * 32 + i * 16 + 4 * q]) =
+            f32x4{v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]};
+    __syncthreads();
+    const bool is_q = n0 < QD;
+    {
+      const int row = threadIdx.x >> 3, jj = threadIdx.x & 7;
+      int64_t r = m0 + row;
+      r = r < a.M ? r : a.M - 1;  // rows past M (not stored) read the last row's tables
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = xs[row][jj + 8 * i];
+      norm_rope_lanes8(x, is_q ? a.qnw : a.knw, F.cos_tab + r * (kHeadD / 2),
+                       F.sin_tab + r * (kHeadD / 2), F.eps, jj);
+      // each lane writes back exactly the elements it read
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xs[row][jj + 8 * i] = x[i];
+    }
+    __syncthreads();
+    if (is_q) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int c = threadIdx.x + 256 * t, row = c >> 5, col = (c & 31) * 4;
+        const int64_t r = m0 + row;
+        if (r < a.M)
+          *reinterpret_cast<f32x4*>(F.q + r * QD + n0 + col) =
+              *reinterpret_cast<const f32x4*>(&xs[row][col]);
+      }
+      return;
+    }
+    const int kvh = (n0 - QD) / kHeadD;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int c = threadIdx.x + 256 * t, row = c >> 4, g = c & 15;
+      const int64_t r = m0 + row;
+      int sg, p;
+      if (r >= a.M || !seg_of(r, sg, p)) continue;
+      const int64_t kb = F.vt_off[sg] / 32 + p / 32;
+      h8 hh, ll;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = xs[row][8 * g + e];
+        bad |= !(fabsf(x) < 65504.f);
+        _Float16 hi, lo;
+        split16(x, hi, lo);
+        hh[e] = hi;
+        ll[e] = lo;
+      }
+      const int64_t at = k_tile_index(kvh, F.nkb, kb, p & 31, 8 * g);
+      *reinterpret_cast<h8*>(F.kh + at) = hh;
+      *reinterpret_cast<h8*>(F.kl + at) = ll;
+    }
+    zero_pad(false, kvh);
+    if (bad) atomicOr(F.overflow, 1u);
+    return;
+  }
+
   if constexpr (MODE == kSiluQuant) {
     // Tiles 4p..4p+3 of the wavefront are gate, up, gate, up rows of 32
     // consecutive h columns (weight_interleave16): lane holds g and u of
@@ -692,6 +839,16 @@ hipError_t launch_cfg16_silu(const GemmArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The fused q/k/v mode: 128-column (one head) x 32-row tiles of four wavefronts.
+hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
+  constexpr int BN = 128, BM = 32;
+  if (a.Kb % 4 || !a.qf || !a.qnw || !a.knw || a.N % BN) return hipErrorInvalidValue;
+  const int64_t n_tiles = a.N / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(256);
+  hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true>), grid, block, 0, st, a);
+  return hipGetLastError();
+}
+
 template <int BN, int BM, int WN, int WM, int SB>
 hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
@@ -706,7 +863,8 @@ hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     case kDumpBlocks:
       hipLaunchKernelGGL((gemm_i8_kernel<BN, BM, WN, WM, SB, kDumpBlocks>), grid, block, 0, st, a);
       break;
-    case kSiluQuant:  // the 16x16 kernel's mode only
+    case kSiluQuant:  // the 16x16 kernel's modes only
+    case kQkvNorm:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -741,6 +899,7 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // with cache-hot weights (17.4 against 18.1 for the next).  At 512 < M < 1024
   // (the LM step, whose weights come cold from HBM) the 256x64 tile of 8
   // wavefronts: 16.0 against 17.4 us with cold weights.
+  if (mode == kQkvNorm) return launch_qkv_norm(a, st);
   if (mode == kSiluQuant) {
     if (a.Kb % 4) return hipErrorInvalidValue;
     if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);

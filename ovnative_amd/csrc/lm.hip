@@ -665,9 +665,13 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   };
   // inputs, contiguous for one upload: ids | audio mask | attention masks
   const size_t ids_bytes = sizeof(int64_t) * (size_t)(T * C);
+  // q/k/v GEMM with qk-norm + RoPE and the K/V planes in its epilogue (the
+  // split attention path with tile-major codes; heads are 128 wide)
+  const bool qkv_fused = tiled && (int)segs.size() <= ovh::kQkvMaxSegs;
   const size_t in_ids = 0, in_am = ids_bytes,                      // byte offsets
                in_mask = in_am + (((size_t)T + 7) & ~(size_t)7),
-               in_bytes = in_mask + (size_t)bias_elems;
+               in_qf = (in_mask + (size_t)bias_elems + 63) & ~(size_t)63,
+               in_bytes = in_qf + (qkv_fused ? sizeof(ovh::QkvFuse) : 0);
   const Buf b_in = take(in_bytes),
             b_bias = take(split ? 0 : sizeof(float) * (size_t)bias_elems),
             b_bits = take(split ? sizeof(uint32_t) * (size_t)bits_words : 0),
@@ -707,6 +711,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   int64_t* d_ids = reinterpret_cast<int64_t*>(d_in + in_ids);
   uint8_t* d_am = reinterpret_cast<uint8_t*>(d_in + in_am);
   uint8_t* d_mask = reinterpret_cast<uint8_t*>(d_in + in_mask);
+  const ovh::QkvFuse* d_qf = reinterpret_cast<const ovh::QkvFuse*>(d_in + in_qf);
   float* x = static_cast<float*>(at(b_x));
   int8_t* aq = static_cast<int8_t*>(at(b_aq));
   float* asc = static_cast<float*>(at(b_asc));
@@ -737,6 +742,27 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     if (bias_off[i] >= 0)
       std::memcpy(L.h_in + in_mask + bias_off[i], segs[i].mask,
                   (size_t)segs[i].rows * (size_t)segs[i].rows);
+  if (qkv_fused) {
+    // the layout-wide part of the fused q/k/v epilogue, uploaded with the inputs
+    ovh::QkvFuse qf{};
+    qf.QD = (int32_t)QD;
+    qf.KVD = (int32_t)KVD;
+    qf.n_segs = (int32_t)segs.size();
+    for (size_t i = 0; i < segs.size(); ++i) {
+      qf.row0[i] = (int32_t)segs[i].row0;
+      qf.rows[i] = segs[i].rows;
+      qf.vt_off[i] = vt_off[i];
+    }
+    qf.nkb = vt_cols / 32;
+    qf.eps = c.rms_eps;
+    qf.q = q;
+    qf.kh = static_cast<_Float16*>(at(b_kh));
+    qf.kl = static_cast<_Float16*>(at(b_kl));
+    qf.vh = static_cast<_Float16*>(at(b_vh));
+    qf.vl = static_cast<_Float16*>(at(b_vl));
+    qf.overflow = L.d_overflow;
+    std::memcpy(L.h_in + in_qf, &qf, sizeof qf);  // the RoPE tables are set below
+  }
   // each segment's mask: bias rows (fp32 attention) or bit words (split form)
   std::vector<OvhAttnSegment> asegs(segs.size());
   std::vector<const uint32_t*> seg_bits(segs.size(), nullptr);
@@ -753,6 +779,11 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   float *cosb = nullptr, *sinb = nullptr;
   int rc = rope_tables_cached(L, pos, T, &cosb, &sinb);
   if (rc != OV_OK) return rc;
+  if (qkv_fused) {
+    ovh::QkvFuse* hq = reinterpret_cast<ovh::QkvFuse*>(L.h_in + in_qf);
+    hq->cos_tab = cosb;
+    hq->sin_tab = sinb;
+  }
 
   const float scale = 1.f / std::sqrt((float)D);
   ovh::AttnArgs aargs{};
@@ -820,9 +851,27 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     float* gu_c[2] = {gate, up};
     for (const OvhLm::Layer& Y : L.layers) {
       if ((rc = norm_q(Y.ln1)) != OV_OK) return rc;
-      if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled)) != OV_OK)
+      if (qkv_fused) {
+        // q/k/v GEMM + qk-norm/RoPE + K/V planes in one launch, then attention
+        ovh::GemmArgs ga;
+        ga.M = (int)T;
+        ga.N = (int)(QD + 2 * KVD);
+        ga.Kb = (int)ovh::kb_of(H);
+        ga.Kp = 32 * ovh::kb_of(H);
+        ga.aq = aq;
+        ga.asc = asc;
+        ga.a_tiled = 1;
+        ga.W = Y.qkv->w.q;
+        ga.ws = Y.qkv->w.scale;
+        ga.qf = d_qf;
+        ga.qnw = Y.qn;
+        ga.knw = Y.kn;
+        OVH_HIP(ovh::launch_gemm(ga, ovh::kQkvNorm, st), "q/k/v + qk-norm launch");
+        OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
+      } else if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled)) !=
+                 OV_OK) {
         return rc;
-      if (split) {
+      } else if (split) {
         // q/k norm + RoPE, f16 planes of k and V, then attention
         OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
                                                sinb, c.rms_eps, aargs, sp, max_rows, st),
