@@ -806,22 +806,33 @@ def run_m16384(args, cfg: dict, tensors) -> None:
     M = B * seq
     lm = ov.LM.from_tensors(tensors, ov.LmConfig(**cfg))
     lm.set_device_sampling(True)
-    for _ in range(args.warmup):
-        lm.forward(ids, am, attn, pos, host_logits=False)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        lm.forward(ids, am, attn, pos, host_logits=False)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    lm.close()
-    ms_step = e0.elapsed_time(e1) / args.steps
+
+    def timed(steps):
+        for _ in range(args.warmup):
+            lm.forward(ids, am, attn, pos, host_logits=False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            lm.forward(ids, am, attn, pos, host_logits=False)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, time.perf_counter() - t0
+
+    ms_step, wall = timed(args.steps)
     ops = linear_ops(cfg, M, args.layers)
     tops = ops / (ms_step * 1e-3) / 1e12
     log(f"M={M} forward {ms_step:.2f} ms ({tops:.1f} linear TOPS)")
+    # the opt-in f16-operand GEMM form on the same forward (same logits bit for bit)
+    prev = ov.set_f16_min_rows(2048)
+    try:
+        ms_f16, _ = timed(max(1, args.steps // 2))
+    finally:
+        ov.set_f16_min_rows(prev)
+    lm.close()
+    log(f"M={M} forward with the f16 GEMM form {ms_f16:.2f} ms "
+        f"({ops / (ms_f16 * 1e-3) / 1e12:.1f} linear TOPS)")
     rs = time_residual(cfg, args.layers, M, reps=1)
     cpu = None if args.no_cpu else cpu_baseline(cfg, tensors, args.cpu_seconds, batch)
     line = {
@@ -847,6 +858,10 @@ def run_m16384(args, cfg: dict, tensors) -> None:
             "parallelism": "single GPU",
             "step_linear_gop": round(ops / 1e9, 2),
             "step_attention_gflop": round(attention_flops(cfg, seq, B, args.layers) / 1e9, 2),
+            "f16_gemm_form": {"ms_per_step": round(ms_f16, 4),
+                              "linear_tops": round(ops / (ms_f16 * 1e-3) / 1e12, 2),
+                              "note": "ovh_set_f16_min_rows(2048): int8-valued f16 operands, "
+                                      "same logits; off by default"},
         },
         "roofline": roofline_entry(
             f"gemm16 residual (o_proj K=2048 and down K=3072; M={M}, N=1024, += x; graph "

@@ -134,6 +134,17 @@ int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const Ovh
  * quantise A (fp32 [M,K]) into a library-owned workspace, then ovh_linear_q. */
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                int accumulate, void* stream);
+/* The f16-operand GEMM form: no counterpart in the reference (a choice of
+ * matrix-core instruction inside this library).  From `rows` rows on (0, the
+ * default: never) the int8 GEMMs (ovh_linear_q, _tiled, _sliced, ovh_linear,
+ * ovh_silu_gate_linear and the LM runner's projections; not
+ * ovh_linear_noalloc) run V_MFMA_F32_16X16X32_F16 on int8-valued f16 copies
+ * of the weights and codes: its fp32 block products are the int32 dots
+ * exactly, so the results are the same bit for bit.  Costs a 2-byte-per-element
+ * f16 copy of each weight (made on its first such call outside graph capture)
+ * and a widened copy of the codes per call.  Process-wide; returns the
+ * previous setting (negative rows: unchanged, a query). */
+int64_t ovh_set_f16_min_rows(int64_t rows);
 /* ovh_linear without any allocation: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The codes and scales

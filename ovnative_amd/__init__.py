@@ -55,6 +55,7 @@ SIGNATURES = {
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
+    "ovh_set_f16_min_rows": (_i64, [_i64]),
     "ovh_weight_gate_up": (_int, [_p, _p, _p, C.POINTER(_p)]),
     "ovh_silu_gate_linear": (_int, [_i64, _p, _p, _p, _p, _p, _p]),
     "ovh_rope_tables": (_int, [_i64, _p, _int, _f32, _p, _p, _p]),
@@ -329,6 +330,13 @@ def linear_q_tiled(aq_tiled, asc, w: Weight, M: int, C=None, accumulate: bool = 
     _check(load().ovh_linear_q_tiled(M, _dptr(aq_tiled), _dptr(asc), w.handle, _dptr(C),
                                      C.shape[1], int(bool(accumulate)), _stream()))
     return C
+
+
+def set_f16_min_rows(rows: int) -> int:
+    """ovh_set_f16_min_rows: GEMMs of at least `rows` rows (0: none, the
+    default) run the f16-operand form, bit-identical to the int8 form; returns
+    the previous setting."""
+    return int(load().ovh_set_f16_min_rows(int(rows)))
 
 
 def linear_q_sliced(aq, asc, w: Weight, slice_n, outs=None):

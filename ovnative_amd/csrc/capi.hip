@@ -6,6 +6,7 @@
 // exception — it becomes a status code plus a per-thread message.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -75,6 +76,54 @@ int check_gemm_operands(int64_t M, const int8_t* aq, const float* asc, const Ovh
   return OV_OK;
 }
 
+std::mutex g_f16_mu;  // making a weight's f16 copy
+std::atomic<int64_t> g_f16_min_rows{0};
+
+// The f16 GEMM form for M rows: the weight's f16 copy (made here on first use)
+// and the codes widened to tile-major f16, into f16_codes when given (2 x
+// ovh_tiled_codes_bytes), else into *ws from the stream-ordered allocator (the
+// caller frees it after the launch).  Leaves a alone where the form does not
+// apply (the form off or M below its row threshold, K not a multiple of 128,
+// no copy made).
+int f16_operands(int64_t M, const int8_t* aq, bool a_tiled, const OvhWeight* w,
+                 _Float16* f16_codes, hipStream_t st, ovh::GemmArgs& a, _Float16** ws,
+                 bool f16_ok = true) {
+  *ws = nullptr;
+  const int64_t min_rows = ovh::f16_min_rows();
+  if (!f16_ok || min_rows <= 0 || M < min_rows || w->w.Kb % 4 != 0 || !ovh::weight_f16(w, st))
+    return OV_OK;
+  const int64_t bytes = (M + 127) / 128 * 128 * w->w.Kp;
+  _Float16* codes = f16_codes;
+  if (!codes) {
+    // no stream-ordered allocation into a graph being captured: int8 form
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return OV_OK;
+    OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(ws), sizeof(_Float16) * (size_t)bytes, st),
+            "hipMallocAsync(f16 codes)");
+    codes = *ws;
+  }
+  const hipError_t e = a_tiled ? ovh::launch_widen_f16(aq, codes, bytes, st)
+                               : ovh::launch_codes_to_f16_tiled(M, w->w.Kp, aq, codes, st);
+  if (e != hipSuccess) {
+    if (*ws) (void)hipFreeAsync(*ws, st);
+    *ws = nullptr;
+    return hip_fail(e, "widen codes to f16");
+  }
+  a.W16 = w->w.q16;
+  a.aq16 = codes;
+  a.a_tiled = 1;
+  return OV_OK;
+}
+
+// Launch, then release the f16 codes workspace (stream order).
+int launch_with_ws(const ovh::GemmArgs& a, ovh::GemmMode mode, _Float16* ws, hipStream_t st) {
+  const hipError_t e = ovh::launch_gemm(a, mode, st);
+  if (ws) (void)hipFreeAsync(ws, st);
+  OVH_HIP(e, "gemm launch");
+  return OV_OK;
+}
+
 ovh::GemmArgs base_args(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w) {
   ovh::GemmArgs a;
   a.M = (int)M;
@@ -91,6 +140,33 @@ ovh::GemmArgs base_args(int64_t M, const int8_t* aq, const float* asc, const Ovh
 }  // namespace
 
 namespace ovh {
+int64_t f16_min_rows() { return g_f16_min_rows.load(std::memory_order_relaxed); }
+void set_f16_min_rows(int64_t rows) { g_f16_min_rows.store(rows, std::memory_order_relaxed); }
+
+bool weight_f16(const OvhWeight* w, hipStream_t st) {
+  if (w->w.q16) return true;
+  // not while a graph is being captured: hipMalloc and the synchronisation
+  // below are not allowed there (the int8 form runs instead)
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  std::lock_guard<std::mutex> lock(g_f16_mu);
+  if (w->w.q16) return true;
+  const int64_t n = w->w.Npad * w->w.Kp;
+  _Float16* p = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&p), sizeof(_Float16) * (size_t)n) != hipSuccess) {
+    (void)hipGetLastError();  // out of memory: keep the int8 form
+    return false;
+  }
+  // finished before any stream may read it
+  if (launch_widen_f16(w->w.q, p, n, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(p);
+    return false;
+  }
+  const_cast<OvhWeight*>(w)->w.q16 = p;
+  return true;
+}
+
 int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
                         OvhWeight** out) {
   *out = nullptr;
@@ -149,7 +225,8 @@ int weight_upload_f32(int64_t N, int64_t K, const float* wsrc, int layout, hipSt
 }
 
 int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
-             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled) {
+             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled, _Float16* f16_codes,
+             bool f16_ok) {
   if (M <= 0) return OV_OK;
   int rc = check_gemm_operands(M, aq, asc, w);
   if (rc != OV_OK) return rc;
@@ -162,13 +239,14 @@ int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, 
   a.start[1] = (int)w->w.N;
   a.out[0] = C;
   a.ld[0] = ldc;
-  OVH_HIP(ovh::launch_gemm(a, accumulate ? ovh::kAccumulate : ovh::kStore, st), "gemm launch");
-  return OV_OK;
+  _Float16* ws = nullptr;
+  if ((rc = f16_operands(M, aq, a_tiled, w, f16_codes, st, a, &ws, f16_ok)) != OV_OK) return rc;
+  return launch_with_ws(a, accumulate ? ovh::kAccumulate : ovh::kStore, ws, st);
 }
 
 int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                     const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
-                    bool a_tiled) {
+                    bool a_tiled, _Float16* f16_codes, bool f16_ok) {
   if (M <= 0 || n_slices <= 0) return OV_OK;
   int rc = check_gemm_operands(M, aq, asc, w);
   if (rc != OV_OK) return rc;
@@ -190,8 +268,9 @@ int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeig
   if (total != w->w.N)
     return fail(OV_ERR_INVALID_ARG, "sliced GEMM: slice widths must sum to the weight's N");
   a.start[n_slices] = (int)total;
-  OVH_HIP(ovh::launch_gemm(a, ovh::kStore, st), "gemm launch");
-  return OV_OK;
+  _Float16* ws = nullptr;
+  if ((rc = f16_operands(M, aq, a_tiled, w, f16_codes, st, a, &ws, f16_ok)) != OV_OK) return rc;
+  return launch_with_ws(a, ovh::kStore, ws, st);
 }
 }  // namespace ovh
 
@@ -315,6 +394,7 @@ void ovh_weight_free(OvhWeight* h) {
   if (!h) return;
   if (h->w.q) (void)hipFree(h->w.q);
   if (h->w.scale) (void)hipFree(h->w.scale);
+  if (h->w.q16) (void)hipFree(h->w.q16);
   if (h->fw.hi) (void)hipFree(h->fw.hi);
   if (h->fw.lo) (void)hipFree(h->fw.lo);
   if (h->fw.scale) (void)hipFree(h->fw.scale);
@@ -534,8 +614,16 @@ int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, 
   int8_t* aq = static_cast<int8_t*>(base);
   float* asc = reinterpret_cast<float*>(static_cast<char*>(base) + code_bytes);
   rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
-  if (rc == OV_OK) rc = ovh_linear_q(M, aq, asc, w, C, ldc, accumulate, stream);
+  // the int8 GEMM form at every M (the f16 form would allocate)
+  if (rc == OV_OK)
+    rc = ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), false, nullptr, false);
   return rc;
+}
+
+int64_t ovh_set_f16_min_rows(int64_t rows) {
+  const int64_t prev = ovh::f16_min_rows();
+  if (rows >= 0) ovh::set_f16_min_rows(rows);
+  return prev;
 }
 
 int ovh_block_dots_tiled(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out,
@@ -579,8 +667,10 @@ int ovh_silu_gate_linear(int64_t M, const int8_t* aq, const float* asc, const Ov
   a.hq = hq;
   a.hsc = hsc;
   a.hKp = gate_up->w.N / 2;  // I, a multiple of 64
-  OVH_HIP(ovh::launch_gemm(a, ovh::kSiluQuant, as_stream(stream)), "silu gate/up launch");
-  return OV_OK;
+  _Float16* ws = nullptr;
+  const int rc = f16_operands(M, aq, false, gate_up, nullptr, as_stream(stream), a, &ws);
+  if (rc != OV_OK) return rc;
+  return launch_with_ws(a, ovh::kSiluQuant, ws, as_stream(stream));
 }
 
 

@@ -44,6 +44,7 @@ struct DeviceWeight {
   int64_t N = 0, K = 0, Npad = 0, Kb = 0, Kp = 0;
   int8_t* q = nullptr;
   float* scale = nullptr;
+  _Float16* q16 = nullptr;  // int8-valued f16 copy of q (same tiles), made on first large-M use
 };
 
 struct GemmArgs {
@@ -68,6 +69,10 @@ struct GemmArgs {
   float* hsc = nullptr;
   int64_t hKp = 0;
   int h_tiled = 0;  // hq tile-major (act_index)
+  // f16-operand form (large M): the weight's int8-valued f16 copy and the
+  // codes widened tile-major (both set, or neither)
+  const _Float16* W16 = nullptr;
+  const _Float16* aq16 = nullptr;
   // kQkvNorm: the layout-wide part in device memory, the layer's norm weights
   const QkvFuse* qf = nullptr;
   const float* qnw = nullptr;
@@ -112,6 +117,17 @@ hipError_t launch_rmsnorm_split(int64_t rows, int64_t cols, const float* x, cons
 hipError_t launch_gemm_f32(const GemmF32Args& a, hipStream_t st);
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);
+// Rows from which the GEMMs take the f16-operand form (GemmArgs::W16/aq16);
+// 0 (the default): never.  Measured on MI355X at M = 16384 the int8 form is the
+// faster one for the plain and residual GEMMs, so the f16 form is opt-in.
+int64_t f16_min_rows();
+void set_f16_min_rows(int64_t rows);
+// int8 -> int8-valued f16 element by element (n % 16 == 0): a weight's tiles or
+// tile-major codes become the f16 form's operands.
+hipError_t launch_widen_f16(const int8_t* src, _Float16* dst, int64_t n, hipStream_t st);
+// row-major int8 codes [M][Kp] -> tile-major f16 codes (rows padded to 128).
+hipError_t launch_codes_to_f16_tiled(int64_t M, int64_t Kp, const int8_t* src, _Float16* dst,
+                                     hipStream_t st);
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
                                 const float* scale_src, DeviceWeight& dst, hipStream_t st);
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st);

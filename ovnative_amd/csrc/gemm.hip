@@ -33,6 +33,8 @@
 // latency on this part is longer than one stage of epilogue work.
 // Workgroups are mapped XCD-aware: the 8 XCDs (blockIdx % 8) each take a
 // contiguous range of weight tiles, so an XCD's L2 holds its own weight slice.
+#include <type_traits>
+
 #include "gemm.h"
 #include "ovh_common.h"
 #include "qk_common.h"
@@ -312,33 +314,56 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_i8_kernel(const GemmArgs a)
 // contiguous bytes; in the row-chunk order of row-major codes chunk
 // (l/32)*32 + row, byte 8*((l/16) & 1) (two rows 8 apart share a bank there).
 
-__device__ __forceinline__ i32x4 mfma16_i8(int64_t a, int64_t b) {
+__device__ __forceinline__ i32x4 mfma16(int64_t a, int64_t b) {
   const i32x4 z = {0, 0, 0, 0};
   return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+// The same block product on int8-valued f16 operands (V_MFMA_F32_16X16X32_F16):
+// every product is an integer of magnitude <= 127^2 and the 32-term sum stays
+// below 2^24, so the fp32 result is the int32 block dot exactly, whatever the
+// order of the matrix core's additions; the epilogue then needs no conversion.
+__device__ __forceinline__ f32x4 mfma16(h8 a, h8 b) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, z, 0, 0, 0);
 }
 
 
 // NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.  PIPE:
 // the stage loop runs as a software pipeline (below); without it each stage
 // is read, multiplied and folded block by block.
-template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE>
+// F16: operands as int8-valued f16 (a.W16, tile-major a.aq16; the int8 tiles
+// widened element by element, so every byte offset doubles): 2 KiB block
+// tiles moved as two 1 KiB DMA units, 16-byte fragments, fp32 block products.
+template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE, bool F16 = false>
 __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int FN = TN / 16, FM = TM / 16;
   static_assert(FN >= 1 && FM >= 1 && TN % 16 == 0 && TM % 16 == 0, "16-row wave tiles");
-  static_assert(BN % 32 == 0 && BM % 32 == 0 && BM <= 64, "32-row block tiles; one scale row per lane");
-  static_assert(SB % 4 == 0 && NST >= 2, "scales move in 16-byte (4-block) chunks");
+  static_assert(BN % 32 == 0 && BM % 32 == 0 && BM <= 128,
+                "32-row block tiles; scale rows one per lane in up to two 64-row halves");
+  static_assert((SB % 4 == 0 || SB == 2) && NST >= 2,
+                "scales move in 16-byte (4-block) chunks, or per block for 2-block stages");
+  static_assert(!F16 || MODE != kDumpBlocks, "block dumps on the int8 operands only");
   constexpr int WT = BN / 32, AT = BM / 32;
-  constexpr int TILES = (WT + AT) * SB;   // 1 KiB block tiles per stage
-  constexpr int SCL = TILES * TILE;       // stage offset of the scales: [SB/4][BM rows][4 floats]
+  constexpr int U = F16 ? 2 : 1;          // 1 KiB DMA units per block tile
+  constexpr int TB = TILE * U;            // bytes per block tile
+  constexpr int FB = F16 ? 16 : 8;        // fragment bytes per lane
+  using Frag = typename std::conditional<F16, h8, int64_t>::type;
+  using Acc = typename std::conditional<F16, f32x4, i32x4>::type;
+  constexpr int TILES = (WT + AT) * SB * U;  // 1 KiB DMA units per stage
+  // stage offset of the scales: [SB/4][BM rows][4 floats], or [2][BM rows] for SB = 2
+  constexpr int SCL = TILES * TILE;
+  constexpr int SCV = SB >= 4 ? SB / 4 : 1;      // f32x4 scale vectors per row and stage
   constexpr int STAGE = SCL + BM * SB * 4;
   constexpr int TPW = (TILES + NW - 1) / NW;
   constexpr bool EVEN = TILES % NW == 0;
   // kDumpBlocks writes each block's int32 products and takes no scales (asc
   // may be null): no scale DMA, so every wavefront's op count is its tiles'
   constexpr bool DUMP = MODE == kDumpBlocks;
-  constexpr int SOPS = DUMP ? 0 : SB / 4;  // scale DMA ops of the last wavefront per stage
+  constexpr int RH = BM > 64 ? 2 : 1;           // 64-row halves of the scale rows
+  constexpr int SPH = SB >= 4 ? SB / 4 : SB;    // scale DMA ops per half and stage
+  constexpr int SOPS = DUMP ? 0 : RH * SPH;     // scale DMA ops of the last wavefront per stage
   __shared__ __attribute__((aligned(16))) int8_t smem[NST][STAGE];
 
   // wave index in a scalar register: the DMA slots and the wait below branch on it
@@ -352,21 +377,25 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   const int64_t Kp = a.Kp;
   const int nstages = Kb / SB;
 
-  // DMA slots of this wavefront: stage tile idx = r * SB + bb (r < WT: weight
-  // row tile, else activation row tile), wavefront w takes idx = w, w + NW, ...
+  // DMA slots of this wavefront: stage unit idx = (r * SB + bb) * U + h (r < WT:
+  // weight row tile, else activation row tile; h: 1 KiB half of an f16 tile),
+  // wavefront w takes idx = w, w + NW, ...
+  const int8_t* const wsrc = F16 ? reinterpret_cast<const int8_t*>(a.W16) : a.W;
+  const int8_t* const asrc = F16 ? reinterpret_cast<const int8_t*>(a.aq16) : a.aq;
   const int8_t* src[TPW];
   int64_t step[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     int idx = wave + t * NW;
     idx = idx < TILES ? idx : TILES - 1;
-    const int bb = idx % SB, r = idx / SB;
+    const int h = idx % U, rb = idx / U;
+    const int bb = rb % SB, r = rb / SB;
     if (r < WT) {
-      src[t] = a.W + ((int64_t)(n0 / 32 + r) * Kb + bb) * TILE + lane * 16;
-      step[t] = (int64_t)SB * TILE;
-    } else if (a.a_tiled) {
-      src[t] = a.aq + ((int64_t)(m0 / 32 + r - WT) * Kb + bb) * TILE + lane * 16;
-      step[t] = (int64_t)SB * TILE;
+      src[t] = wsrc + ((int64_t)(n0 / 32 + r) * Kb + bb) * TB + h * TILE + lane * 16;
+      step[t] = (int64_t)SB * TB;
+    } else if (F16 || a.a_tiled) {
+      src[t] = asrc + ((int64_t)(m0 / 32 + r - WT) * Kb + bb) * TB + h * TILE + lane * 16;
+      step[t] = (int64_t)SB * TB;
     } else {
       int row = m0 + (r - WT) * 32 + (lane & 31);
       row = row < a.M ? row : a.M - 1;  // rows are independent: clamp, discard later
@@ -374,14 +403,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       step[t] = SB * 32;
     }
   }
-  const float* ssrc = nullptr;
+  const float* ssrc[RH] = {};
   if (!DUMP) {
-    int row = m0 + lane;
-    row = row < a.M ? row : a.M - 1;
-    ssrc = a.asc + (int64_t)row * Kb;
+#pragma unroll
+    for (int h = 0; h < RH; ++h) {
+      int row = m0 + 64 * h + lane;
+      row = row < a.M ? row : a.M - 1;
+      ssrc[h] = a.asc + (int64_t)row * Kb;
+    }
   }
   // Stage s -> ring slot s % NST.  The last wavefront also moves the scales
-  // (SB/4 more DMA ops); a wavefront's DMA ops complete in issue order.
+  // (SOPS more DMA ops); a wavefront's DMA ops complete in issue order.
   auto issue = [&](int s) __attribute__((always_inline)) {
     int8_t* base = smem[s % NST];
 #pragma unroll
@@ -391,17 +423,26 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(src[t] + s * step[t]),
                                          (lds_void_t*)(base + idx * TILE), 16, 0, 0);
     }
-    if (!DUMP && wave == NW - 1 && lane < BM) {
+    if (!DUMP && wave == NW - 1 && (RH == 2 || lane < BM)) {
 #pragma unroll
-      for (int c = 0; c < SB / 4; ++c)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc + s * SB + 4 * c),
-                                         (lds_void_t*)(base + SCL + c * BM * 16), 16, 0, 0);
+      for (int h = 0; h < RH; ++h)
+#pragma unroll
+        for (int c = 0; c < SPH; ++c) {
+          if constexpr (SB >= 4)
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc[h] + s * SB + 4 * c),
+                                             (lds_void_t*)(base + SCL + c * BM * 16 + h * 1024),
+                                             16, 0, 0);
+          else
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(ssrc[h] + s * SB + c),
+                                             (lds_void_t*)(base + SCL + c * BM * 4 + h * 256), 4,
+                                             0, 0);
+        }
     }
   };
   // Waiting for stage s: the DMA ops this wavefront issued after it (stages
   // s+1 .. s+NST-2) may stay in flight.  Per stage, wavefronts below
   // TILES % NW issue TPW ops, the others TPW - 1 (all TPW when EVEN), and the
-  // last one SB/4 more for the scales; each waits on its own count, since a
+  // last one SOPS more for the scales; each waits on its own count, since a
   // smaller one would also wait for part of the next stage.
   constexpr int OPS_HI = TPW, OPS_LO = EVEN ? TPW : TPW - 1;
   constexpr int LATER_HI = OPS_HI * (NST - 2), LATER_LO = OPS_LO * (NST - 2);
@@ -416,13 +457,14 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int t16 = wn * FN + i;
-    aoff[i] = (t16 >> 1) * SB * TILE + (t16 & 1) * 512 + 8 * lane;
+    aoff[i] = (t16 >> 1) * SB * TB + (t16 & 1) * (TB / 2) + FB * lane;
   }
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int t16 = wm * FM + j;
-    boff[j] = (WT + (t16 >> 1)) * SB * TILE +
-              (a.a_tiled ? (t16 & 1) * 512 + 8 * lane : (t16 & 1) * 16 * 16 + frag_rows);
+    boff[j] = (WT + (t16 >> 1)) * SB * TB +
+              ((F16 || a.a_tiled) ? (t16 & 1) * (TB / 2) + FB * lane
+                                  : (t16 & 1) * 16 * 16 + frag_rows);
   }
 
   f32x4 f[FN][FM];
@@ -436,9 +478,25 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   // block products go to the matrix core.  Fragments, scales and block
   // products of a stage are held in registers between those steps; the
   // epilogue still folds the blocks into f in block order.
-  int64_t af[SB][FN], bf[SB][FM];
-  f32x4 sc[SB / 4][FM], sc_next[SB / 4][FM];
-  i32x4 acc[SB][FN][FM];
+  Frag af[SB][FN], bf[SB][FM];
+  f32x4 sc[SCV][FM], sc_next[SCV][FM];
+  // scales of a stage for this wavefront's rows: sc[bb / 4][j][bb % 4] for block bb
+  auto load_scales = [&](const int8_t* base, f32x4 (&scs)[SCV][FM]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      const int row = wm * TM + 16 * j + (lane & 15);
+      if constexpr (SB >= 4) {
+#pragma unroll
+        for (int c = 0; c < SB / 4; ++c)
+          scs[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 + row * 16);
+      } else {
+#pragma unroll
+        for (int c = 0; c < SB; ++c)
+          scs[0][j][c] = *reinterpret_cast<const float*>(base + SCL + c * BM * 4 + row * 4);
+      }
+    }
+  };
+  Acc acc[SB][FN][FM];
   // Stage s in LDS for every wavefront: this wavefront's DMA for it landed
   // (and its own LDS reads, so its slot reads are done), then the others'.
   // A bare s_barrier: __syncthreads()'s release fence would also drain the
@@ -456,22 +514,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     }
     __builtin_amdgcn_s_barrier();
   };
-  auto read_stage = [&](int s, f32x4 (&scs)[SB / 4][FM]) __attribute__((always_inline)) {
+  auto read_stage = [&](int s, f32x4 (&scs)[SCV][FM]) __attribute__((always_inline)) {
     const int8_t* base = smem[s % NST];
-#pragma unroll
-    for (int c = 0; c < SB / 4; ++c)
-#pragma unroll
-      for (int j = 0; j < FM; ++j)
-        scs[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
-                                                    (wm * TM + 16 * j + (lane & 15)) * 16);
+    load_scales(base, scs);
 #pragma unroll
     for (int bb = 0; bb < SB; ++bb) {
 #pragma unroll
       for (int i = 0; i < FN; ++i)
-        af[bb][i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
+        af[bb][i] = *reinterpret_cast<const Frag*>(base + aoff[i] + bb * TB);
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        bf[bb][j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+        bf[bb][j] = *reinterpret_cast<const Frag*>(base + boff[j] + bb * TB);
     }
   };
   auto products = [&]() __attribute__((always_inline)) {
@@ -480,7 +533,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j) acc[bb][i][j] = mfma16_i8(af[bb][i], bf[bb][j]);
+        for (int j = 0; j < FM; ++j) acc[bb][i][j] = mfma16(af[bb][i], bf[bb][j]);
   };
   // kDumpBlocks: block b's int32 product of output (m, n) to dump[(m N + n) Kb + b]
   auto dump_block = [&](const i32x4& p, int i, int j, int b) __attribute__((always_inline)) {
@@ -525,7 +578,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       epilogue(s);
       products();
 #pragma unroll
-      for (int c = 0; c < SB / 4; ++c)
+      for (int c = 0; c < SCV; ++c)
 #pragma unroll
         for (int j = 0; j < FM; ++j) sc[c][j] = sc_next[c][j];
     }
@@ -537,26 +590,21 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       // wavefront has left
       if (s + NST - 1 < nstages) issue(s + NST - 1);
       const int8_t* base = smem[s % NST];
-#pragma unroll
-      for (int c = 0; c < SB / 4; ++c)
-#pragma unroll
-        for (int j = 0; j < FM; ++j)
-          sc[c][j] = *reinterpret_cast<const f32x4*>(base + SCL + c * BM * 16 +
-                                                     (wm * TM + 16 * j + (lane & 15)) * 16);
+      load_scales(base, sc);
 #pragma unroll
       for (int bb = 0; bb < SB; ++bb) {
-        int64_t a1[FN], b1[FM];
+        Frag a1[FN], b1[FM];
 #pragma unroll
         for (int i = 0; i < FN; ++i)
-          a1[i] = *reinterpret_cast<const int64_t*>(base + aoff[i] + bb * TILE);
+          a1[i] = *reinterpret_cast<const Frag*>(base + aoff[i] + bb * TB);
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          b1[j] = *reinterpret_cast<const int64_t*>(base + boff[j] + bb * TILE);
+          b1[j] = *reinterpret_cast<const Frag*>(base + boff[j] + bb * TB);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
           for (int j = 0; j < FM; ++j) {
-            const i32x4 p = mfma16_i8(a1[i], b1[j]);
+            const Acc p = mfma16(a1[i], b1[j]);
             if constexpr (DUMP) {
               dump_block(p, i, j, s * SB + bb);
             } else {
@@ -839,13 +887,48 @@ hipError_t launch_cfg16_silu(const GemmArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The f16-operand form (int8-valued f16 weights and codes, tile-major): the
+// exact block products come out of the f16 MFMA as fp32, so the epilogue has
+// no int -> float conversion.  Store, residual and SiLU modes.
+template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
+hipError_t launch_cfg16_f16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
+  if (a.Kb % SB || !a.a_tiled) return hipErrorInvalidValue;
+  const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(64 * WN * WM);
+  switch (mode) {
+    case kStore:
+      hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kStore, PIPE, true>), grid, block,
+                         0, st, a);
+      break;
+    case kAccumulate:
+      hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumulate, PIPE, true>), grid,
+                         block, 0, st, a);
+      break;
+    case kSiluQuant:
+      if constexpr (BN / WN == 64) {
+        if (a.N % 128 || !a.hq || !a.hsc || a.hKp < a.N / 2) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemm16_kernel<BN, BM, WN, WM, SB, NST, kSiluQuant, PIPE, true>), grid,
+                           block, 0, st, a);
+        break;
+      }
+      return hipErrorInvalidValue;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // The fused q/k/v mode: 128-column (one head) x 32-row tiles of four wavefronts.
 hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
   constexpr int BN = 128, BM = 32;
   if (a.Kb % 4 || !a.qf || !a.qnw || !a.knw || a.N % BN) return hipErrorInvalidValue;
   const int64_t n_tiles = a.N / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
   const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(256);
-  hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true>), grid, block, 0, st, a);
+  if (a.W16 && a.aq16)
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true, true>), grid, block, 0, st,
+                       a);
+  else
+    hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true>), grid, block, 0, st, a);
   return hipGetLastError();
 }
 
@@ -900,6 +983,16 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // (the LM step, whose weights come cold from HBM) the 256x64 tile of 8
   // wavefronts: 16.0 against 17.4 us with cold weights.
   if (mode == kQkvNorm) return launch_qkv_norm(a, st);
+  if ((a.W16 != nullptr) != (a.aq16 != nullptr)) return hipErrorInvalidValue;
+  if (a.W16) {
+    // f16 form (sweep at M = 16384, N = 1024..8200, K = 1024..3072, MI355X):
+    // 128 x 128 tiles of 8 wavefronts (64 x 32 each), 2-block stages in a
+    // 2-stage ring (68 KB of LDS: the f16 tiles are twice the int8 ones), the
+    // block-by-block loop; 560-714 TOPS against 690-830 for the int8 form's
+    // 128 x 64 tiles, and 683 against 641 for the SiLU-fused gate/up
+    if (a.Kb % 4 || mode == kDumpBlocks) return hipErrorInvalidValue;
+    return launch_cfg16_f16<128, 128, 2, 4, 2, 2, false>(a, mode, st);
+  }
   if (mode == kSiluQuant) {
     if (a.Kb % 4) return hipErrorInvalidValue;
     if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);
@@ -1049,6 +1142,56 @@ hipError_t launch_weight_interleave16(const DeviceWeight& gate, const DeviceWeig
   e = hipMemsetAsync(dst.q + 2 * gate.N * dst.Kp, 0, (size_t)((dst.Npad - 2 * gate.N) * dst.Kp), st);
   if (e != hipSuccess) return e;
   return hipMemsetAsync(dst.scale + 2 * gate.N, 0, sizeof(float) * (size_t)(dst.Npad - 2 * gate.N), st);
+}
+
+// int8 -> int8-valued f16, element by element (an int8 tile layout becomes the
+// f16 one: byte offset x 2).  16 values per thread.
+__global__ void widen_f16_kernel(const int8_t* __restrict__ src, _Float16* __restrict__ dst,
+                                 int64_t n16) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n16) return;
+  const i32x4 v = *reinterpret_cast<const i32x4*>(src + 16 * t);
+  h8 lo, hi;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    lo[e] = (_Float16)(float)(int8_t)(v[e >> 2] >> (8 * (e & 3)));
+    hi[e] = (_Float16)(float)(int8_t)(v[2 + (e >> 2)] >> (8 * (e & 3)));
+  }
+  *reinterpret_cast<h8*>(dst + 16 * t) = lo;
+  *reinterpret_cast<h8*>(dst + 16 * t + 8) = hi;
+}
+
+// Row-major int8 codes [M][Kp] -> tile-major f16 codes (act_index order, rows
+// padded to a multiple of 128 with zeros).  One thread per 8 codes of a row.
+__global__ void codes_to_f16_tiled_kernel(int64_t M, int64_t Mp, int64_t Kp,
+                                          const int8_t* __restrict__ src,
+                                          _Float16* __restrict__ dst) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = Kp / 8;
+  if (t >= Mp * per_row) return;
+  const int64_t m = t / per_row, k = (t - m * per_row) * 8;
+  int64_t v = 0;
+  if (m < M) v = *reinterpret_cast<const int64_t*>(src + m * Kp + k);
+  h8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (_Float16)(float)(int8_t)(v >> (8 * e));
+  *reinterpret_cast<h8*>(dst + act_index(m, k, Kp, true)) = o;  // 8 codes of one row piece
+}
+
+hipError_t launch_widen_f16(const int8_t* src, _Float16* dst, int64_t n, hipStream_t st) {
+  if (n % 16) return hipErrorInvalidValue;
+  const int64_t n16 = n / 16;
+  hipLaunchKernelGGL(widen_f16_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st, src,
+                     dst, n16);
+  return hipGetLastError();
+}
+
+hipError_t launch_codes_to_f16_tiled(int64_t M, int64_t Kp, const int8_t* src, _Float16* dst,
+                                     hipStream_t st) {
+  const int64_t Mp = (M + 127) / 128 * 128, n = Mp * (Kp / 8);
+  hipLaunchKernelGGL(codes_to_f16_tiled_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     M, Mp, Kp, src, dst);
+  return hipGetLastError();
 }
 
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st) {

@@ -641,6 +641,16 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // (K a multiple of 128: H, and inter for down)
   const bool tiled = split && L.silu_fused && H % 256 == 0 && H <= 1024 && I % 128 == 0;
   const int64_t Tpad = (T + 127) / 128 * 128;
+  // From f16_min_rows() rows (when set) the GEMMs take int8-valued f16
+  // operands: every int8 weight gets its f16 copy (made once, before any
+  // capture) and the codes are widened into one arena buffer ahead of each GEMM.
+  const int64_t f16_rows = ovh::f16_min_rows();
+  bool f16 = tiled && f16_rows > 0 && T >= f16_rows;
+  for (const OvhLm::Layer& Y : L.layers)
+    if (f16)
+      f16 = ovh::weight_f16(Y.qkv, L.st) && ovh::weight_f16(Y.o, L.st) &&
+            ovh::weight_f16(Y.gate_up, L.st) && ovh::weight_f16(Y.down, L.st);
+  if (f16 && !L.head->f32) f16 = ovh::weight_f16(L.head, L.st);
   std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
   int64_t bias_elems = 0, bits_words = 0;
   for (size_t i = 0; i < segs.size(); ++i) {
@@ -685,6 +695,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // fp32 head: the final norm's output as f16 hi/lo planes and row scales
   const bool head_f32 = L.head->f32;
   const size_t hplane = head_f32 ? sizeof(_Float16) * (size_t)ovh::f32_plane_halves(T, H) : 0;
+  const Buf b_aq16 = take(f16 ? sizeof(_Float16) * (size_t)(Tpad * Kp_max) : 0);
   const Buf b_hh = take(hplane), b_hl = take(hplane),
             b_hs = take(head_f32 ? sizeof(float) * (size_t)Tpad : 0);
   // split-f16 attention planes (K and V tile-major, segments padded to 32 keys)
@@ -722,6 +733,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   float* gate = static_cast<float*>(at(b_g));
   float* up = static_cast<float*>(at(b_u));
   float* logits = static_cast<float*>(at(b_lg));
+  _Float16* aq16 = f16 ? static_cast<_Float16*>(at(b_aq16)) : nullptr;
   hipStream_t st = L.st;
 
   // stage the inputs in pinned memory (after the previous upload has left it)
@@ -866,10 +878,15 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         ga.qf = d_qf;
         ga.qnw = Y.qn;
         ga.knw = Y.kn;
+        if (f16) {
+          OVH_HIP(ovh::launch_widen_f16(aq, aq16, Tpad * ga.Kp, st), "widen codes");
+          ga.W16 = Y.qkv->w.q16;
+          ga.aq16 = aq16;
+        }
         OVH_HIP(ovh::launch_gemm(ga, ovh::kQkvNorm, st), "q/k/v + qk-norm launch");
         OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
-      } else if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled)) !=
-                 OV_OK) {
+      } else if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled, aq16,
+                                            f16)) != OV_OK) {
         return rc;
       } else if (split) {
         // q/k norm + RoPE, f16 planes of k and V, then attention
@@ -886,7 +903,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           return rc;
       }
       if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
-      if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled)) != OV_OK) return rc;
+      if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled, aq16, f16)) != OV_OK) return rc;
       if ((rc = norm_q(Y.ln2)) != OV_OK) return rc;
       if (L.silu_fused) {
         // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
@@ -905,8 +922,14 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         ga.hKp = I;
         ga.a_tiled = tiled;
         ga.h_tiled = tiled;
+        if (f16) {
+          OVH_HIP(ovh::launch_widen_f16(aq, aq16, Tpad * ga.Kp, st), "widen codes");
+          ga.W16 = Y.gate_up->w.q16;
+          ga.aq16 = aq16;
+        }
         OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
-        if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled)) != OV_OK) return rc;
+        if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled, aq16, f16)) != OV_OK)
+          return rc;
       } else {
         if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
         if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
@@ -938,7 +961,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     }
     if ((rc = norm_q(L.final_norm)) != OV_OK)
       return rc;
-    return ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled);
+    return ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled, aq16, f16);
   };
 
   if (!L.use_graphs) {
@@ -948,7 +971,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     // and every buffer address the launches take.  A changed layout (other
     // lengths, a grown arena, new RoPE tables) is captured anew; the same
     // layout replays over the new inputs the upload above brought.
-    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, (int64_t)segs.size(),
+    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, f16, (int64_t)segs.size(),
                                 (int64_t)in_bytes, (int64_t)(intptr_t)L.arena,
                                 (int64_t)(intptr_t)cosb, (int64_t)(intptr_t)sinb};
     for (size_t i = 0; i < segs.size(); ++i) {

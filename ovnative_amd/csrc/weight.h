@@ -24,12 +24,22 @@ namespace ovh {
 int weight_interleave16(const OvhWeight* gate, const OvhWeight* up, hipStream_t st,
                         OvhWeight** out);
 // ovh_linear_q / ovh_linear_q_sliced, with the codes aq tile-major
-// (act_index; rows up to a multiple of 128 readable) when a_tiled.
+// (act_index; rows up to a multiple of 128 readable) when a_tiled.  From
+// f16_min_rows() rows (when set; K a multiple of 128) they run the f16-operand
+// GEMM form:
+// the codes are widened into f16_codes when given (2 x ovh_tiled_codes_bytes),
+// else into a stream-ordered allocation.  f16_ok = false keeps the int8 form.
 int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* C,
-             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled);
+             int64_t ldc, int accumulate, hipStream_t st, bool a_tiled,
+             _Float16* f16_codes = nullptr, bool f16_ok = true);
 int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                     const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
-                    bool a_tiled);
+                    bool a_tiled, _Float16* f16_codes = nullptr, bool f16_ok = true);
+// The int8-valued f16 copy of w's tiles (DeviceWeight::q16) for the large-M
+// GEMM form, made on first call (hipMalloc, widened on st, then st synchronised;
+// serialised over threads).  False where it cannot be made now: during graph
+// capture on st, or out of device memory; the int8 form then runs.
+bool weight_f16(const OvhWeight* w, hipStream_t st);
 // fp32 weight from host memory, OVW1 layout 0 ([N,K]) or 1 ([K,N])
 int weight_upload_f32(int64_t N, int64_t K, const float* w, int layout, hipStream_t st,
                       OvhWeight** out);

@@ -38,6 +38,17 @@ def test_pure_host_entry_points():
     assert lib.ovh_last_error() == b""
 
 
+def test_f16_form_switch():
+    """The f16-operand GEMM form is off by default; the setter returns the
+    previous threshold and a negative value only queries."""
+    import ovnative_amd as ov
+    assert ov.set_f16_min_rows(-1) == 0
+    assert ov.set_f16_min_rows(4096) == 0
+    assert ov.set_f16_min_rows(-1) == 4096
+    assert ov.set_f16_min_rows(0) == 4096
+    assert ov.set_f16_min_rows(-1) == 0
+
+
 def test_argument_errors_without_device():
     """Argument checks run before any device work, so they are testable here."""
     import ovnative_amd as ov

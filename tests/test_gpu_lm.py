@@ -104,14 +104,21 @@ def test_forward_bit_exact_given_attention(oracle, small_lm, split, seq):
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
-def test_large_batch_bit_exact_given_attention(oracle, small_lm):
-    """M = 4 x 600 = 2400 rows: the runner takes its large-M GEMM tiles (128 x 64,
-    block-by-block stage loop, for q/k/v, the residual projections and the
-    SiLU-fused gate/up) and the logits stay identical to the oracle's forward
-    given the device attention."""
+@pytest.mark.parametrize("f16_rows", [0, 2048], ids=["int8_form", "f16_form"])
+def test_large_batch_bit_exact_given_attention(oracle, small_lm, f16_rows):
+    """M = 4 x 600 = 2400 rows: the runner takes its large-M GEMM tiles (128 x
+    64 int8, or with the f16 form switched on int8-valued f16 operands in 128 x
+    128 tiles, for q/k/v with its fused epilogue, the residual projections, the
+    SiLU-fused gate/up and the head) and the logits stay identical to the
+    oracle's forward given the device attention."""
+    import ovnative_amd as ov
     ts, table, lm = small_lm
     ids, am, attn, pos = make_inputs(23, SMALL, 4, 600, 20)
-    got = lm.forward(ids, am, attn, pos)
+    prev = ov.set_f16_min_rows(f16_rows)
+    try:
+        got = lm.forward(ids, am, attn, pos)
+    finally:
+        ov.set_f16_min_rows(prev)
     B, Cb, S, V = got.shape
     flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
     segs = [(attn[b], S, b * S) for b in range(B)]
@@ -199,6 +206,29 @@ def test_full_width_layer_bit_exact_given_attention(oracle):
     try:
         got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
     finally:
+        lm.close()
+    B, Cb, S, V = got.shape
+    flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)
+    segs = [(attn[b], S, b * S) for b in range(B)]
+    hybrid = oracle.lm_forward(FULL1, table, ids, am, segs, pos.reshape(-1),
+                               attention=_device_attention(FULL1))
+    assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+
+
+def test_full_width_f16_form_bit_exact_given_attention(oracle):
+    """One layer at the LM's real widths with M = 2 x 1024 = 2048 rows and the f16
+    GEMM form switched on from 2048 rows (every projection, the fused q/k/v
+    epilogue and the 8 x 1025 head take it): logits identical to the oracle's
+    forward given the device attention."""
+    import ovnative_amd as ov
+    ts, table = make_lm(13, FULL1)
+    ids, am, attn, pos = make_inputs(17, FULL1, 2, 1024, 64)
+    lm = ov.LM.from_tensors(ts, _cfg(FULL1))
+    prev = ov.set_f16_min_rows(2048)
+    try:
+        got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
+    finally:
+        ov.set_f16_min_rows(prev)
         lm.close()
     B, Cb, S, V = got.shape
     flat = got.transpose(0, 2, 1, 3).reshape(B * S, Cb * V)

@@ -243,6 +243,109 @@ def test_large_m_properties(oracle):
 
 
 # ---------------------------------------------------------------------------
+# the f16-operand GEMM form (opt-in, here from 2048 rows): int8-valued f16
+# weights and codes, exact block products out of the f16 matrix core.  Rows are
+# independent, so the int8 form over row chunks below the threshold gives every
+# row's expected bits at full size; sampled rows are checked against the oracle
+# as well.
+
+F16_MIN_ROWS = 2048
+
+
+@pytest.fixture
+def f16_form():
+    import ovnative_amd as ov
+    prev = ov.set_f16_min_rows(F16_MIN_ROWS)
+    assert prev == 0  # off unless asked for
+    yield
+    ov.set_f16_min_rows(prev)
+
+
+def _by_chunks(M, fn, chunk=1024):
+    assert chunk < F16_MIN_ROWS
+    for r0 in range(0, M, chunk):
+        fn(r0, min(M, r0 + chunk))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 1024), (16384, 4096, 1024), (4133, 1024, 3072),
+                                   (16384, 8200, 1024), (2111, 1024, 2048), (3000, 96, 128)])
+def test_f16_form_equals_int8_form(oracle, f16_form, M, N, K):
+    """Store and residual forms, row-major and tile-major codes: every row of the
+    f16 form equals the int8 form's, sampled rows equal the oracle (q/k/v N = 4096,
+    the head's 8200 columns, K = 2048 / 3072 of o_proj / down, ragged M)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(M + 3 * N + K)
+    A, Wf = _rand_problem(rng, M, N, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    C = ov.linear_q(aq, asc, w)
+    ref = torch.empty_like(C)
+
+    def part(r0, r1):
+        ref[r0:r1] = ov.linear_q(aq[r0:r1], asc[r0:r1], w)
+    _by_chunks(M, part)
+    C_h = host(C)
+    assert np.array_equal(bits(C_h), bits(host(ref)))
+    rows = np.sort(rng.choice(M, 32, replace=False))
+    assert np.array_equal(bits(C_h[rows]), bits(_oracle_linear(oracle, A[rows], q, s)))
+    del C, ref
+    Cin = rng.standard_normal((M, N)).astype(np.float32)
+    c1, c2 = dev(Cin), dev(Cin)
+    ov.linear_q_tiled(ov.tile_major(aq), asc, w, M, c1, accumulate=True)
+
+    def part_acc(r0, r1):
+        ov.linear_q(aq[r0:r1], asc[r0:r1], w, c2[r0:r1], accumulate=True)
+    _by_chunks(M, part_acc)
+    assert np.array_equal(bits(host(c1)), bits(host(c2)))
+
+
+def test_f16_form_sliced(oracle, f16_form):
+    """The sliced GEMM (q/k/v into three outputs) in the f16 form."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(31)
+    M, K = 3000, 1024
+    A, Wf = _rand_problem(rng, M, 4096, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    outs = ov.linear_q_sliced(aq, asc, w, [2048, 1024, 1024])
+    full = host(ov.linear_q(aq[:1000], asc[:1000], w))
+    got = np.concatenate([host(o) for o in outs], axis=1)
+    assert np.array_equal(bits(got[:1000]), bits(full))
+    rows = np.sort(rng.choice(M, 16, replace=False))
+    assert np.array_equal(bits(got[rows]), bits(_oracle_linear(oracle, A[rows], q, s)))
+
+
+def test_f16_form_silu_gate_linear(oracle, f16_form):
+    """The SiLU-fused gate/up at M = 16384 (config 5, N = 2 x 3072): codes and
+    scales of every row equal the int8 form's, sampled rows the oracle's
+    composition (sliced GEMM, then silu_mul_quantize_f32)."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(61)
+    M, I, K = 16384, 3072, 1024
+    A = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    qg, sg = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    qu, su = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    gu = ov.gate_up_weight(ov.Weight.from_host(qg, sg), ov.Weight.from_host(qu, su))
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    hq, hsc = ov.silu_gate_linear(aq, asc, gu)
+    hq2, hsc2 = torch.empty_like(hq), torch.empty_like(hsc)
+
+    def part(r0, r1):
+        a, b = ov.silu_gate_linear(aq[r0:r1], asc[r0:r1], gu)
+        hq2[r0:r1], hsc2[r0:r1] = a, b
+    _by_chunks(M, part)
+    hq, hsc = host(hq), host(hsc)
+    assert np.array_equal(hq, host(hq2)) and np.array_equal(bits(hsc), bits(host(hsc2)))
+    rows = np.sort(rng.choice(M, 24, replace=False))
+    hq_r, hsc_r = oracle.silu_mul_quantize(_oracle_linear(oracle, A[rows], qg, sg),
+                                           _oracle_linear(oracle, A[rows], qu, su))
+    assert np.array_equal(hq[rows], u8_to_s8(hq_r, I))
+    assert np.array_equal(bits(hsc[rows]), bits(hsc_r))
+
+
+# ---------------------------------------------------------------------------
 # fused producers at LM shapes vs the oracle
 
 @pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (40, 256), (7, 512),
