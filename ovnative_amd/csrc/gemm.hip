@@ -620,13 +620,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   if constexpr (DUMP) return;
 
   if constexpr (MODE == kQkvNorm) {
-    // One head (128 columns) of 32 rows per workgroup; wavefront wn holds
-    // columns 32 wn .. +31.  The values are those the sliced store would write
-    // (f * wscale); then, as qk_norm_rope_f32 and the plane split do them:
-    // v heads straight to the V planes, q and k heads through LDS (8 lanes per
-    // head vector, norm_rope_lanes8), q stored fp32, k to the K planes.
-    static_assert(BN == 128 && BM == 32 && WM == 1 && NW == 4 && FN == 2 && FM == 2,
-                  "kQkvNorm: 128 x 32 tiles of four wavefronts");
+    // One head (128 columns) of BM rows per workgroup; wavefront (wn, wm) holds
+    // columns 32 wn .. +31 of rows 32 wm .. +31.  The values are those the
+    // sliced store would write (f * wscale); then, as qk_norm_rope_f32 and the
+    // plane split do them: v heads straight to the V planes, q and k heads
+    // through LDS (8 lanes per head vector, norm_rope_lanes8), q stored fp32,
+    // k to the K planes.
+    static_assert(BN == 128 && WN == 4 && FN == 2 && FM == 2 && 64 * NW == 8 * BM,
+                  "kQkvNorm: 128-column tiles, 32 x 32 per wavefront, 8 threads per row");
+    constexpr int NT = 64 * NW;
     const QkvFuse& F = *a.qf;
     const int QD = F.QD, KVD = F.KVD;
     float v[FN][FM][4];
@@ -679,7 +681,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
       const int kvh = (n0 - QD - KVD) / kHeadD;
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        const int64_t r = m0 + j * 16 + (lane & 15);
+        const int64_t r = m0 + (wm * FM + j) * 16 + (lane & 15);
         int sg, p;
         if (r >= a.M || !seg_of(r, sg, p)) continue;
         const int64_t kb = F.vt_off[sg] / 32 + p / 32;
@@ -704,12 +706,12 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     // has left the K loop)
     __syncthreads();
     float(*xs)[kHeadD + 4] = reinterpret_cast<float(*)[kHeadD + 4]>(&smem[0][0]);
-    static_assert(BM * (kHeadD + 4) * 4 <= STAGE, "the staged head fits in one ring slot");
+    static_assert(BM * (kHeadD + 4) * 4 <= NST * STAGE, "the staged head fits in the ring");
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int j = 0; j < FM; ++j)
-        *reinterpret_cast<f32x4*>(&xs[j * 16 + (lane & 15)][wn * 32 + i * 16 + 4 * q]) =
+        *reinterpret_cast<f32x4*>(&xs[(wm * FM + j) * 16 + (lane & 15)][wn * 32 + i * 16 + 4 * q]) =
             f32x4{v[i][j][0], v[i][j][1], v[i][j][2], v[i][j][3]};
     __syncthreads();
     const bool is_q = n0 < QD;
@@ -729,8 +731,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     __syncthreads();
     if (is_q) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int c = threadIdx.x + 256 * t, row = c >> 5, col = (c & 31) * 4;
+      for (int t = 0; t < BM * 32 / NT; ++t) {
+        const int c = threadIdx.x + NT * t, row = c >> 5, col = (c & 31) * 4;
         const int64_t r = m0 + row;
         if (r < a.M)
           *reinterpret_cast<f32x4*>(F.q + r * QD + n0 + col) =
@@ -740,8 +742,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
     }
     const int kvh = (n0 - QD) / kHeadD;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int c = threadIdx.x + 256 * t, row = c >> 4, g = c & 15;
+    for (int t = 0; t < BM * 16 / NT; ++t) {
+      const int c = threadIdx.x + NT * t, row = c >> 4, g = c & 15;
       const int64_t r = m0 + row;
       int sg, p;
       if (r >= a.M || !seg_of(r, sg, p)) continue;
@@ -918,18 +920,24 @@ hipError_t launch_cfg16_f16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The fused q/k/v mode: 128-column (one head) x 32-row tiles of four wavefronts.
-hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
-  constexpr int BN = 128, BM = 32;
-  if (a.Kb % 4 || !a.qf || !a.qnw || !a.knw || a.N % BN) return hipErrorInvalidValue;
+// The fused q/k/v mode: 128-column (one head) tiles, 32 rows of four wavefronts
+// (pipelined stage loop), or from 2048 rows 64 rows of eight (block by block,
+// as the large-M store tiles).
+template <int BM, bool PIPE, bool F16>
+hipError_t launch_qkv_cfg(const GemmArgs& a, hipStream_t st) {
+  constexpr int BN = 128;
   const int64_t n_tiles = a.N / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
-  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(256);
-  if (a.W16 && a.aq16)
-    hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true, true>), grid, block, 0, st,
-                       a);
-  else
-    hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, 1, 4, 2, kQkvNorm, true>), grid, block, 0, st, a);
+  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(8 * BM);
+  hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, BM / 32, 4, 2, kQkvNorm, PIPE, F16>), grid, block, 0,
+                     st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
+  if (a.Kb % 4 || !a.qf || !a.qnw || !a.knw || a.N % 128) return hipErrorInvalidValue;
+  if (a.W16 && a.aq16) return launch_qkv_cfg<32, true, true>(a, st);
+  if (a.M >= 2048) return launch_qkv_cfg<64, false, false>(a, st);
+  return launch_qkv_cfg<32, true, false>(a, st);
 }
 
 template <int BN, int BM, int WN, int WM, int SB>

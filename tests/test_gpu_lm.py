@@ -215,16 +215,18 @@ def test_full_width_layer_bit_exact_given_attention(oracle):
     assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
 
 
-def test_full_width_f16_form_bit_exact_given_attention(oracle):
-    """One layer at the LM's real widths with M = 2 x 1024 = 2048 rows and the f16
-    GEMM form switched on from 2048 rows (every projection, the fused q/k/v
-    epilogue and the 8 x 1025 head take it): logits identical to the oracle's
-    forward given the device attention."""
+@pytest.mark.parametrize("f16_rows", [0, 2048], ids=["int8_form", "f16_form"])
+def test_full_width_large_m_bit_exact_given_attention(oracle, f16_rows):
+    """One layer at the LM's real widths with M = 2 x 1024 = 2048 rows, where the
+    large-M tiles start (the fused q/k/v epilogue on 64-row tiles), in the int8
+    form and with the f16 GEMM form switched on from 2048 rows (every
+    projection, the fused q/k/v epilogue and the 8 x 1025 head take it): logits
+    identical to the oracle's forward given the device attention."""
     import ovnative_amd as ov
     ts, table = make_lm(13, FULL1)
     ids, am, attn, pos = make_inputs(17, FULL1, 2, 1024, 64)
     lm = ov.LM.from_tensors(ts, _cfg(FULL1))
-    prev = ov.set_f16_min_rows(2048)
+    prev = ov.set_f16_min_rows(f16_rows)
     try:
         got = lm.forward(ids, am, attn, pos)              # [B, C, S, V]
     finally:
