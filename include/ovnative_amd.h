@@ -130,6 +130,24 @@ int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhW
 int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                         const int64_t* slice_n, float* const* slice_c, int n_slices,
                         void* stream);
+/* One launch over up to 8 independent ovh_linear_q problems (each its own
+ * codes, scales, weight, output and M; all in the store form, or all in the
+ * residual form: accumulate applies to every member).  No counterpart in the
+ * reference, which runs such GEMMs one after another
+ * (linear_s8_nk_packed_q, gemm.cpp:758-774, one call per projection in
+ * lm.cpp:241-311); the results are those of ovh_linear_q bit for bit.  For
+ * the skinny shapes (M < 256), where one launch per GEMM leaves most of the
+ * GPU waiting on launch latency instead of streaming weights.  Every member's
+ * K must be a multiple of 128 (OV_ERR_NOT_IMPLEMENTED otherwise). */
+typedef struct OvhGemmGroup {
+  int64_t M;
+  const int8_t* aq;  /* row-major codes [M][Kp] */
+  const float* asc;  /* [M][Kb] */
+  const OvhWeight* w;
+  float* C;          /* [M][ldc] */
+  int64_t ldc;
+} OvhGemmGroup;
+int ovh_linear_q_grouped(const OvhGemmGroup* groups, int n_groups, int accumulate, void* stream);
 /* linear_s8_nk_packed / _packed_add (ov_gemm.h:67-75, gemm.cpp:829-845, :864-882):
  * quantise A (fp32 [M,K]) into a library-owned workspace, then ovh_linear_q. */
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,

@@ -56,6 +56,7 @@ SIGNATURES = {
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
     "ovh_set_f16_min_rows": (_i64, [_i64]),
+    "ovh_linear_q_grouped": (_int, [_p, _int, _int, _p]),
     "ovh_weight_gate_up": (_int, [_p, _p, _p, C.POINTER(_p)]),
     "ovh_silu_gate_linear": (_int, [_i64, _p, _p, _p, _p, _p, _p]),
     "ovh_rope_tables": (_int, [_i64, _p, _int, _f32, _p, _p, _p]),
@@ -330,6 +331,26 @@ def linear_q_tiled(aq_tiled, asc, w: Weight, M: int, C=None, accumulate: bool = 
     _check(load().ovh_linear_q_tiled(M, _dptr(aq_tiled), _dptr(asc), w.handle, _dptr(C),
                                      C.shape[1], int(bool(accumulate)), _stream()))
     return C
+
+
+class GemmGroup(C.Structure):
+    _fields_ = [("M", C.c_int64), ("aq", C.c_void_p), ("asc", C.c_void_p), ("w", C.c_void_p),
+                ("C", C.c_void_p), ("ldc", C.c_int64)]
+
+
+def linear_q_grouped(problems, outs=None, accumulate: bool = False):
+    """ovh_linear_q_grouped: problems = [(aq, asc, Weight), ...] (row-major codes),
+    one launch; returns the outputs ([M, N] fp32 each, or `outs` updated)."""
+    torch = _torch()
+    if outs is None:
+        outs = [torch.empty((aq.shape[0], w.N), dtype=torch.float32, device="cuda")
+                for aq, _, w in problems]
+    arr = (GemmGroup * max(1, len(problems)))()
+    for i, ((aq, asc, w), c) in enumerate(zip(problems, outs)):
+        arr[i] = GemmGroup(aq.shape[0], _dptr(aq).value, _dptr(asc).value, w.handle.value,
+                           _dptr(c).value, c.shape[1])
+    _check(load().ovh_linear_q_grouped(arr, len(problems), int(bool(accumulate)), _stream()))
+    return outs
 
 
 def set_f16_min_rows(rows: int) -> int:

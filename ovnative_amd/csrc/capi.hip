@@ -514,6 +514,37 @@ int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const Ovh
   return ovh::linear_q_sliced(M, aq, asc, w, slice_n, slice_c, n_slices, as_stream(stream), false);
 }
 
+int ovh_linear_q_grouped(const OvhGemmGroup* groups, int n_groups, int accumulate,
+                         void* stream) {
+  if (n_groups <= 0) return OV_OK;
+  if (!groups) return fail(OV_ERR_INVALID_ARG, "groups is null");
+  if (n_groups > ovh::kMaxGroups)
+    return fail(OV_ERR_INVALID_ARG, "grouped GEMM: at most 8 groups");
+  ovh::GemmGroups gg;
+  for (int g = 0; g < n_groups; ++g) {
+    const OvhGemmGroup& m = groups[g];
+    if (m.M <= 0) continue;  // an empty member: nothing to launch
+    int rc = check_gemm_operands(m.M, m.aq, m.asc, m.w);
+    if (rc != OV_OK) return rc;
+    if (!m.C) return fail(OV_ERR_INVALID_ARG, "C is null");
+    if (m.ldc < m.w->w.N) return fail(OV_ERR_INVALID_ARG, "ldc < N");
+    if (m.w->w.Kb % 4 != 0)
+      return fail(OV_ERR_NOT_IMPLEMENTED, "grouped GEMM: K must be a multiple of 128");
+    ovh::GemmArgs a = base_args(m.M, m.aq, m.asc, m.w);
+    a.nslices = 1;
+    a.start[0] = 0;
+    a.start[1] = (int)m.w->w.N;
+    a.out[0] = m.C;
+    a.ld[0] = m.ldc;
+    gg.args[gg.n++] = a;
+  }
+  if (gg.n == 0) return OV_OK;
+  OVH_HIP(ovh::launch_gemm_grouped(gg, accumulate ? ovh::kAccumulate : ovh::kStore,
+                                   as_stream(stream)),
+          "grouped gemm launch");
+  return OV_OK;
+}
+
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                int accumulate, void* stream) {
   if (M <= 0) return OV_OK;

@@ -117,6 +117,15 @@ hipError_t launch_rmsnorm_split(int64_t rows, int64_t cols, const float* x, cons
 hipError_t launch_gemm_f32(const GemmF32Args& a, hipStream_t st);
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st);
+// Up to kMaxGroups independent GEMMs (store or residual mode, K a multiple of
+// 128, int8 form) in one launch; start[] is filled in by the launcher.
+constexpr int kMaxGroups = 8;
+struct GemmGroups {
+  int n = 0;
+  int start[kMaxGroups + 1] = {};
+  GemmArgs args[kMaxGroups];
+};
+hipError_t launch_gemm_grouped(const GemmGroups& gg, GemmMode mode, hipStream_t st);
 // Rows from which the GEMMs take the f16-operand form (GemmArgs::W16/aq16);
 // 0 (the default): never.  Measured on MI355X at M = 16384 the int8 form is the
 // faster one for the plain and residual GEMMs, so the f16 form is opt-in.

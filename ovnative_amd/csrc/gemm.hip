@@ -334,8 +334,10 @@ __device__ __forceinline__ f32x4 mfma16(h8 a, h8 b) {
 // F16: operands as int8-valued f16 (a.W16, tile-major a.aq16; the int8 tiles
 // widened element by element, so every byte offset doubles): 2 KiB block
 // tiles moved as two 1 KiB DMA units, 16-byte fragments, fp32 block products.
+// The body of one workgroup's output tile; wg is the workgroup's index in its
+// GEMM's grid (grouped launches offset it).
 template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE, bool F16 = false>
-__global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) {
+__device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int FN = TN / 16, FM = TM / 16;
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   const int wn = wave % WN, wm = wave / WN;
   const int n_tiles = (a.N + BN - 1) / BN;
   int ntile, mtile;
-  if (!tile_of(blockIdx.x, n_tiles, ntile, mtile)) return;  // padding workgroup
+  if (!tile_of(wg, n_tiles, ntile, mtile)) return;  // padding workgroup
   const int n0 = ntile * BN, m0 = mtile * BM;
   const int Kb = a.Kb;
   const int64_t Kp = a.Kp;
@@ -860,6 +862,21 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) 
   }
 }
 
+template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE, bool F16 = false>
+__global__ __launch_bounds__(64 * WN * WM) void gemm16_kernel(const GemmArgs a) {
+  gemm16_tile<BN, BM, WN, WM, SB, NST, MODE, PIPE, F16>(a, blockIdx.x);
+}
+
+// Several independent GEMMs in one launch: GEMM g takes the workgroups
+// start[g] .. start[g + 1] - 1 (each range a whole padded grid of grid_size(),
+// a multiple of 8, so the XCD of a workgroup is that of its local index).
+template <int BN, int BM, int WN, int WM, int SB, int NST, int MODE, bool PIPE>
+__global__ __launch_bounds__(64 * WN * WM) void gemm16_grouped_kernel(const GemmGroups gg) {
+  int g = 0;
+  while (g + 1 < gg.n && (int)blockIdx.x >= gg.start[g + 1]) ++g;
+  gemm16_tile<BN, BM, WN, WM, SB, NST, MODE, PIPE>(gg.args[g], (int)blockIdx.x - gg.start[g]);
+}
+
 // Launchable when Kb % SB == 0.
 template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
 hipError_t launch_cfg16(const GemmArgs& a, GemmMode mode, hipStream_t st) {
@@ -969,7 +986,48 @@ hipError_t launch_cfg(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   return launch_cfg_sb<BN, BM, WN, WM, 1>(a, mode, st);
 }
 
+template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
+hipError_t launch_grouped_cfg(GemmGroups gg, GemmMode mode, hipStream_t st) {
+  int total = 0;
+  for (int g = 0; g < gg.n; ++g) {
+    const GemmArgs& a = gg.args[g];
+    if (a.Kb % SB) return hipErrorInvalidValue;
+    const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+    gg.start[g] = total;
+    total += (int)grid_size(n_tiles, m_tiles);
+  }
+  gg.start[gg.n] = total;
+  const dim3 grid((unsigned)total), block(64 * WN * WM);
+  if (mode == kAccumulate)
+    hipLaunchKernelGGL((gemm16_grouped_kernel<BN, BM, WN, WM, SB, NST, kAccumulate, PIPE>), grid,
+                       block, 0, st, gg);
+  else
+    hipLaunchKernelGGL((gemm16_grouped_kernel<BN, BM, WN, WM, SB, NST, kStore, PIPE>), grid, block,
+                       0, st, gg);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_gemm_grouped(const GemmGroups& gg, GemmMode mode, hipStream_t st) {
+  if (gg.n <= 0 || gg.n > kMaxGroups || (mode != kStore && mode != kAccumulate))
+    return hipErrorInvalidValue;
+  int64_t max_m = 0;
+  bool kb8 = true;
+  for (int g = 0; g < gg.n; ++g) {
+    const GemmArgs& a = gg.args[g];
+    if (a.Kb % 4 || a.W16 || a.M <= 0) return hipErrorInvalidValue;
+    max_m = a.M > max_m ? a.M : max_m;
+    kb8 = kb8 && a.Kb % 8 == 0;
+  }
+  // one tile shape for every member: the skinny one (the seven projections of a
+  // layer at M = 128) below 256 rows, the large-M one from 2048, the 32 x 32
+  // tile of four wavefronts between
+  if (max_m < 256 && kb8) return launch_grouped_cfg<32, 32, 2, 2, 8, 3, true>(gg, mode, st);
+  if (max_m < 256) return launch_grouped_cfg<32, 32, 2, 2, 4, 3, true>(gg, mode, st);
+  if (max_m >= 2048) return launch_grouped_cfg<128, 64, 4, 2, 4, 2, false>(gg, mode, st);
+  return launch_grouped_cfg<32, 32, 2, 2, 4, 2, true>(gg, mode, st);
+}
 
 hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // Tile choice, from a sweep of every config on MI355X over the LM shapes

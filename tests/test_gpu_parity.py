@@ -346,6 +346,64 @@ def test_f16_form_silu_gate_linear(oracle, f16_form):
 
 
 # ---------------------------------------------------------------------------
+# grouped launch: several independent GEMMs, each member's bits those of its own
+# ovh_linear_q
+
+def test_linear_q_grouped_equals_separate(oracle):
+    """The seven projections of a layer at M = 128 in one
+    launch, then members of ragged M (1, 37, 300: other tile bands) with the
+    residual form; every member equals ovh_linear_q, one against the oracle."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(12)
+    H, QD, KVD, I = 1024, 2048, 1024, 3072
+    shapes = [(QD, H), (KVD, H), (KVD, H), (H, QD), (I, H), (I, H), (H, I)]
+    acts = {}
+    probs, hostw = [], []
+    for n, k in shapes:
+        if k not in acts:
+            acts[k] = rng.standard_normal((128, k)).astype(np.float32)
+        q, s = oracle.quantize_weight_rows((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        hostw.append((q, s))
+        aq, asc = ov.s8_nk_quantize(dev(acts[k]))
+        probs.append((aq, asc, ov.Weight.from_host(q, s)))
+    outs = ov.linear_q_grouped(probs)
+    for (aq, asc, w), c in zip(probs, outs):
+        assert np.array_equal(bits(host(c)), bits(host(ov.linear_q(aq, asc, w))))
+    q, s = hostw[3]
+    assert np.array_equal(bits(host(outs[3])), bits(_oracle_linear(oracle, acts[QD], q, s)))
+    # ragged M, residual form
+    mixed = []
+    for M, (n, k) in [(1, (1024, 1024)), (37, (512, 2048)), (300, (1024, 3072))]:
+        A = rng.standard_normal((M, k)).astype(np.float32)
+        q, s = oracle.quantize_weight_rows((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        mixed.append((aq, asc, ov.Weight.from_host(q, s)))
+    cins = [rng.standard_normal((p[0].shape[0], p[2].N)).astype(np.float32) for p in mixed]
+    got = [dev(c) for c in cins]
+    ov.linear_q_grouped(mixed, got, accumulate=True)
+    for (aq, asc, w), g, c in zip(mixed, got, cins):
+        want = dev(c)
+        ov.linear_q(aq, asc, w, want, accumulate=True)
+        assert np.array_equal(bits(host(g)), bits(host(want)))
+
+
+def test_linear_q_grouped_errors(oracle):
+    import ovnative_amd as ov
+    rng = np.random.default_rng(3)
+    q, s = oracle.quantize_weight_rows((rng.standard_normal((64, 96)) * 0.1).astype(np.float32))
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(rng.standard_normal((5, 96)).astype(np.float32)))
+    with pytest.raises(ov.OvhError):       # K = 96: not a multiple of 128
+        ov.linear_q_grouped([(aq, asc, w)])
+    q2, s2 = oracle.quantize_weight_rows((rng.standard_normal((64, 128)) * 0.1).astype(np.float32))
+    w2 = ov.Weight.from_host(q2, s2)
+    aq2, asc2 = ov.s8_nk_quantize(dev(rng.standard_normal((5, 128)).astype(np.float32)))
+    with pytest.raises(ov.InvalidArgument):  # nine members
+        ov.linear_q_grouped([(aq2, asc2, w2)] * 9)
+    assert ov.linear_q_grouped([]) == []
+
+
+# ---------------------------------------------------------------------------
 # fused producers at LM shapes vs the oracle
 
 @pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (40, 256), (7, 512),
