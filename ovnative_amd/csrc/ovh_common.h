@@ -48,12 +48,30 @@ __device__ __forceinline__ int quant_q(float v, float inv) {
 // again correctly rounded (53 >= 2*24 + 2, so the double rounding is innocuous).
 __device__ __forceinline__ float sqrt_rn(float x) { return (float)__dsqrt_rn((double)x); }
 
-// Max over the 8 lanes of an aligned 8-lane group (one 32-k block, 4 values per lane).
+// Max over the 8 lanes of an aligned 8-lane group (one 32-k block, 4 values per
+// lane), by DPP lane moves (no LDS round trip): the pair (quad_perm 1,0,3,2),
+// the quad (quad_perm 2,3,0,1), then the other quad of the 8 (row_half_mirror:
+// lane i of the 8 reads lane 7 - i).  The max of a set does not depend on the
+// order it is taken in.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float group8_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1, 8));
-  v = fmaxf(v, __shfl_xor(v, 2, 8));
-  v = fmaxf(v, __shfl_xor(v, 4, 8));
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
   return v;
+}
+
+// sum_{j<8} of lane j's p, added in lane order (every lane gets it); the lane
+// values are read as scalars (v_readlane), not through LDS.
+__device__ __forceinline__ float sum_lanes8_in_order(float p) {
+  float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 0));
+#pragma unroll
+  for (int j = 1; j < 8; ++j)
+    sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j)));
+  return sum;
 }
 
 // One 32-k block spread over an 8-lane group, 4 values per lane: computes the

@@ -198,9 +198,7 @@ __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* 
     }
     part = acc;
   }
-  float sum = __shfl(part, 0);
-#pragma unroll
-  for (int j = 1; j < 8; ++j) sum = __fadd_rn(sum, __shfl(part, j));
+  const float sum = sum_lanes8_in_order(part);
   const float scale =
       __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
 #pragma unroll
