@@ -94,6 +94,65 @@ __device__ __forceinline__ float quant_block_lane(const float v[4], int nvalid, 
   return __fdiv_rn(amax, 127.0f);
 }
 
+// RMSNorm + block quantisation of one row of 256*P columns (P <= 4) by one
+// wavefront (lane = the lane index), as rmsnorm_quantize_f32 computes it
+// (cpp/src/backend/cpu/gemm.cpp:638-707; the same order as the general
+// rmsnorm_quantize_kernel): lane l owns
+// k = 256p + 4l..+3, which is also the 4-value slot of quantisation block
+// 8p + l/8, so the row never has to be re-read.  For the sum of squares the
+// row is staged in LDS (xt: kRmsRowLds<P> floats of this wavefront's own)
+// transposed, chain j (elements j, j+8, ...) as one contiguous run, and lanes
+// 0..7 stream their chains with ds_read_b128; the 8 chains are added in order.
+template <int P>
+constexpr int kRmsRowLds = 8 * (32 * P + 4);
+template <int P>
+__device__ __forceinline__ void rms_quant_row(const float* __restrict__ row,
+                                              const float* __restrict__ w, float eps,
+                                              int8_t* __restrict__ aq, float* __restrict__ asc,
+                                              int64_t r, bool tiled, int lane, float* xt) {
+  constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
+  f32x4 xv[P], wv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) xv[p] = *reinterpret_cast<const f32x4*>(row + 256 * p + 4 * lane);
+#pragma unroll
+  for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
+  // element 256p + 4l + c -> chain 4(l&1) + c, position 32p + l/2
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xt[(4 * (lane & 1) + c) * TP + 32 * p + (lane >> 1)] = xv[p][c];
+  // the writes of the other lanes of this wavefront land before the reads
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float part = 0.f;
+  if (lane < 8) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < T; t += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&xt[lane * TP + t]);
+      acc = fmaf(v[0], v[0], acc);
+      acc = fmaf(v[1], v[1], acc);
+      acc = fmaf(v[2], v[2], acc);
+      acc = fmaf(v[3], v[3], acc);
+    }
+    part = acc;
+  }
+  const float sum = sum_lanes8_in_order(part);
+  const float scale =
+      __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(xv[p][i], scale), wv[p][i]);
+    uint32_t codes;
+    const float s = quant_block_lane(v, 4, &codes);
+    *reinterpret_cast<uint32_t*>(aq + act_index(r, 256 * p + 4 * lane, cols, tiled)) = codes;
+    if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
+  }
+}
+
 // silu(g) * u as the reference's exp256 lanes compute it (ops_cpu.cpp:75-92,
 // 144-198 as its GCC build compiles them: the range reduction x - n*ln2 and
 // the final "1 + p*2^n" are fused).

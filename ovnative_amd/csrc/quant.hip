@@ -156,12 +156,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(int64_t rows, int
   }
 }
 
-// Rows of 256*P columns (P <= 4; the LM's hidden sizes), one wavefront per row:
-// lane l owns k = 256p + 4l..+3, which is also the 4-value slot of quantisation
-// block 8p + l/8, so the row never has to be re-read.  For the sum of squares
-// the row is staged in LDS transposed, chain j (elements j, j+8, ...) as one
-// contiguous run, and lanes 0..7 stream their chains with ds_read_b128.  Same
-// arithmetic, in the same order, as rmsnorm_quantize_kernel.
+// Rows of 256*P columns (P <= 4; the LM's hidden sizes), one wavefront per row
+// (rms_quant_row, shared with the residual GEMM's fused row norm).
 template <int P>
 __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* __restrict__ x,
                                                                    const float* __restrict__ w,
@@ -169,48 +165,9 @@ __global__ __launch_bounds__(64) void rmsnorm_quantize_rows_kernel(const float* 
                                                                    int8_t* __restrict__ aq,
                                                                    float* __restrict__ asc,
                                                                    bool tiled) {
-  constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
-  __shared__ __attribute__((aligned(16))) float xt[8 * TP];
-  const int lane = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float xt[kRmsRowLds<P>];
   const int64_t r = blockIdx.x;
-  const float* row = x + r * cols;
-  f32x4 xv[P], wv[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) xv[p] = *reinterpret_cast<const f32x4*>(row + 256 * p + 4 * lane);
-#pragma unroll
-  for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
-  // element 256p + 4l + c -> chain 4(l&1) + c, position 32p + l/2
-#pragma unroll
-  for (int p = 0; p < P; ++p)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) xt[(4 * (lane & 1) + c) * TP + 32 * p + (lane >> 1)] = xv[p][c];
-  __syncthreads();
-  float part = 0.f;
-  if (lane < 8) {
-    float acc = 0.f;
-#pragma unroll 8
-    for (int t = 0; t < T; t += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&xt[lane * TP + t]);
-      acc = fmaf(v[0], v[0], acc);
-      acc = fmaf(v[1], v[1], acc);
-      acc = fmaf(v[2], v[2], acc);
-      acc = fmaf(v[3], v[3], acc);
-    }
-    part = acc;
-  }
-  const float sum = sum_lanes8_in_order(part);
-  const float scale =
-      __fdiv_rn(1.f, sqrt_rn(__fadd_rn(__fdiv_rn(sum, (float)cols), eps)));
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(__fmul_rn(xv[p][i], scale), wv[p][i]);
-    uint32_t codes;
-    const float s = quant_block_lane(v, 4, &codes);
-    *reinterpret_cast<uint32_t*>(aq + act_index(r, 256 * p + 4 * lane, cols, tiled)) = codes;
-    if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
-  }
+  rms_quant_row<P>(x + r * 256 * P, w, eps, aq, asc, r, tiled, threadIdx.x, xt);
 }
 
 // ---------------------------------------------------------------------------
