@@ -59,6 +59,12 @@ typedef struct OvhWeight OvhWeight;
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* ovh_last_error(void);
+/* The same message into a caller-owned buffer, the reference's C ABI
+ * convention (`char* err, size_t err_len` of ov_engine_create / ov_tts,
+ * cpp/include/ovnative/ovnative.h:42-57): at most err_len - 1 bytes and a NUL
+ * (nothing when err is NULL or err_len is 0); returns the message's full
+ * length, so a caller can tell it was truncated. */
+size_t ovh_copy_last_error(char* err, size_t err_len);
 
 /* ABI version and the device the library runs on, e.g. "hip:gfx950 (256 CUs)".
  * Plays the role of ov_engine_backend() (cpp/include/ovnative/ovnative.h:49)

@@ -56,6 +56,7 @@ SIGNATURES = {
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
     "ovh_set_f16_min_rows": (_i64, [_i64]),
+    "ovh_copy_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "ovh_linear_q_grouped": (_int, [_p, _int, _int, _p]),
     "ovh_weight_gate_up": (_int, [_p, _p, _p, C.POINTER(_p)]),
     "ovh_silu_gate_linear": (_int, [_i64, _p, _p, _p, _p, _p, _p]),

@@ -278,6 +278,15 @@ extern "C" {
 
 const char* ovh_last_error(void) { return t_err.c_str(); }
 
+size_t ovh_copy_last_error(char* err, size_t err_len) {
+  if (err && err_len > 0) {
+    const size_t n = t_err.size() < err_len - 1 ? t_err.size() : err_len - 1;
+    std::memcpy(err, t_err.data(), n);
+    err[n] = '\0';
+  }
+  return t_err.size();
+}
+
 int ovh_abi_version(void) { return OVH_ABI_VERSION; }
 
 int ovh_backend_name(char* buf, size_t len) {

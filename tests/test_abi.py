@@ -38,6 +38,23 @@ def test_pure_host_entry_points():
     assert lib.ovh_last_error() == b""
 
 
+def test_copy_last_error_caller_buffer():
+    """The reference's convention: the message into a caller-owned buffer,
+    truncated with a NUL, the full length returned."""
+    import ovnative_amd as ov
+    lib = ov.load()
+    h = ctypes.c_void_p()
+    assert lib.ovh_weight_upload(0, 5, None, None, 0, None, ctypes.byref(h)) == ov.OV_ERR_INVALID_ARG
+    msg = lib.ovh_last_error()
+    n = len(msg)
+    buf = ctypes.create_string_buffer(256)
+    assert lib.ovh_copy_last_error(buf, 256) == n and buf.value == msg
+    small = ctypes.create_string_buffer(b"x" * 8)
+    assert lib.ovh_copy_last_error(small, 5) == n
+    assert small.raw[:5] == msg[:4] + b"\0"
+    assert lib.ovh_copy_last_error(None, 0) == n
+
+
 def test_f16_form_switch():
     """The f16-operand GEMM form is off by default; the setter returns the
     previous threshold and a negative value only queries."""
