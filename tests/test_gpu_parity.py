@@ -387,6 +387,24 @@ def test_linear_q_grouped_equals_separate(oracle):
         assert np.array_equal(bits(host(g)), bits(host(want)))
 
 
+@pytest.mark.parametrize("Ms", [(600, 601, 37), (2100, 128, 5)], ids=["mid", "large"])
+def test_linear_q_grouped_tile_bands(oracle, Ms):
+    """The grouped launch takes one tile shape for all members, chosen by the
+    largest M (32x32 tiles in the mid band, 128x64 tiles from 2048 rows): every
+    member, small ones included, still equals its own ovh_linear_q."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(sum(Ms))
+    probs = []
+    for M, (n, k) in zip(Ms, [(1024, 2048), (4096, 1024), (1024, 3072)]):
+        A = rng.standard_normal((M, k)).astype(np.float32)
+        q, s = oracle.quantize_weight_rows((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        probs.append((aq, asc, ov.Weight.from_host(q, s)))
+    outs = ov.linear_q_grouped(probs)
+    for (aq, asc, w), c in zip(probs, outs):
+        assert np.array_equal(bits(host(c)), bits(host(ov.linear_q(aq, asc, w))))
+
+
 def test_linear_q_grouped_errors(oracle):
     import ovnative_amd as ov
     rng = np.random.default_rng(3)
