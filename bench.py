@@ -44,8 +44,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-# CPU baseline placement: OpenMP threads bound close
-# to the cores they start on, one per core; set before any OpenMP runtime starts.
+# CPU baseline placement: OpenMP threads bound close to the cores they start
+# on, one per core; set before any OpenMP runtime starts.
 os.environ.setdefault("OMP_PROC_BIND", "close")
 os.environ.setdefault("OMP_PLACES", "cores")
 try:  # the CPUs this process may use, read before OpenMP binds the main thread
@@ -899,7 +899,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is described in DESIGN.md, not launched.", file=sys.stderr)
+              "multi-GPU sharding is designed, not launched, in this build.", file=sys.stderr)
         sys.exit(2)
     import torch
     import ovnative_amd as ov

@@ -1,4 +1,5 @@
-"""The reference-side C++ shims of INTEGRATION.md compile against the
+"""The reference-side C++ shims of the repository's integration guide (every
+```cpp block of the top-level guide the test reads) compile against the
 reference's own headers (cpp/src/model/lm.h, tts.h, ov_weights.h) and
 include/ovnative_amd.h, and the runner thunks have exactly the plugin's
 function-pointer types (static_asserts in the shim: LM::CudaForwardFn,
