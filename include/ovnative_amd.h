@@ -361,6 +361,12 @@ void ovh_lm_set_attention(OvhLm* lm, int split_f16);
  * (default), 0 = launched one by one.  Both give the same bits.  No reference
  * counterpart (the CUDA runner launches its kernels one by one). */
 void ovh_lm_set_graphs(OvhLm* lm, int on);
+/* o_proj and down with the RMSNorm + quantise that follows each of them in the
+ * same launch: 1 = where the layout allows it (default; below 2048 rows, int8
+ * GEMM form, tile-major codes), 0 = the norm as a launch of its own.  Both give
+ * the same bits.  No reference counterpart (lm.cpp:339-401 runs the norm as a
+ * step of its own). */
+void ovh_lm_set_fused_norm(OvhLm* lm, int on);
 /* LmRunnerSampleThunk (cuda_lm.h:39-41): the per-step guidance + argmax pass
  * (tts.cpp:296-326) on device logit planes; pred/scores host [C, target_len]. */
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

@@ -83,6 +83,7 @@ SIGNATURES = {
                                    _i64, _p]),
     "ovh_lm_set_attention": (None, [_p, _int]),
     "ovh_lm_set_graphs": (None, [_p, _int]),
+    "ovh_lm_set_fused_norm": (None, [_p, _int]),
 }
 
 
@@ -612,6 +613,10 @@ class LM:
     def set_graphs(self, on: bool) -> None:
         """Replay the forward as a captured HIP graph (default) or launch its kernels one by one."""
         load().ovh_lm_set_graphs(self.handle, int(bool(on)))
+
+    def set_fused_norm(self, on: bool) -> None:
+        """Run each RMSNorm after o_proj / down in the same launch (default) or as its own."""
+        load().ovh_lm_set_fused_norm(self.handle, int(bool(on)))
 
     def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
                target_len: int, guidance: float, layer_penalty: float):

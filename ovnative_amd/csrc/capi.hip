@@ -244,6 +244,33 @@ int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, 
   return launch_with_ws(a, accumulate ? ovh::kAccumulate : ovh::kStore, ws, st);
 }
 
+int linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
+                  int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
+                  unsigned long long* band_cnt, uint32_t* err, hipStream_t st) {
+  if (M <= 0) return OV_OK;
+  int rc = check_gemm_operands(M, aq, asc, w);
+  if (rc != OV_OK) return rc;
+  if (!x || !nw || !nq || !nsc || !band_cnt || !err)
+    return fail(OV_ERR_INVALID_ARG, "residual + norm GEMM: null operand");
+  if (ldx < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldx < N");
+  ovh::GemmArgs a = base_args(M, aq, asc, w);
+  a.a_tiled = 1;
+  a.nslices = 1;
+  a.start[0] = 0;
+  a.start[1] = (int)w->w.N;
+  a.out[0] = x;
+  a.ld[0] = ldx;
+  a.nw = nw;
+  a.neps = eps;
+  a.nq = nq;
+  a.nsc = nsc;
+  a.n_tiled = 1;
+  a.band_cnt = band_cnt;
+  a.norm_err = err;
+  OVH_HIP(ovh::launch_gemm(a, ovh::kAccumNorm, st), "residual + norm gemm launch");
+  return OV_OK;
+}
+
 int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                     const int64_t* slice_n, float* const* slice_c, int n_slices, hipStream_t st,
                     bool a_tiled, _Float16* f16_codes, bool f16_ok) {

@@ -11,7 +11,26 @@ constexpr int kMaxSlices = 8;
 // N-tile the kernels use (32..128 rows) reads in-bounds rows and zero scales.
 constexpr int kRowPad = 128;
 
-enum GemmMode { kStore = 0, kAccumulate = 1, kDumpBlocks = 2, kSiluQuant = 3, kQkvNorm = 4 };
+enum GemmMode {
+  kStore = 0,
+  kAccumulate = 1,
+  kDumpBlocks = 2,
+  kSiluQuant = 3,
+  kQkvNorm = 4,
+  kAccumNorm = 5
+};
+
+// kAccumNorm: the residual GEMM (kAccumulate, one output slice) followed by
+// rmsnorm_quantize of the rows it updated.  Each 32-row tile of the output (a
+// band) is computed by workgroups of one XCD; each counts itself in its
+// band's counter once its stores are in that XCD's L2, and the last
+// kNormHelpers to arrive wait for the count to complete and normalise the
+// band's rows.  The counters are 64-bit, kBandCntStride words apart, zero
+// when allocated, and advance by the number of column tiles per launch.
+constexpr int kNormHelpers = 8;
+constexpr int kBandCntStride = 32;
+// 64-bit words of band counters for M rows
+inline int64_t band_counter_words(int64_t M) { return (M + 31) / 32 * kBandCntStride; }
 
 // kQkvNorm: the runner's merged q/k/v GEMM with qk_norm_rope_f32 and the
 // split-f16 attention's K/V planes in its epilogue.  Each 128-column output
@@ -77,6 +96,16 @@ struct GemmArgs {
   const QkvFuse* qf = nullptr;
   const float* qnw = nullptr;
   const float* knw = nullptr;
+  // kAccumNorm: norm weight and eps, codes [M][N] (tile-major when n_tiled)
+  // and scales [M][N / 32] of the normalised rows (N = 256 P, P <= 4), the
+  // band counters, and a flag that gets bit 2 if a helper's wait ran out
+  const float* nw = nullptr;
+  float neps = 0.f;
+  int8_t* nq = nullptr;
+  float* nsc = nullptr;
+  int n_tiled = 0;
+  unsigned long long* band_cnt = nullptr;
+  uint32_t* norm_err = nullptr;
 };
 
 // fp32 linear on the f16 matrix cores (gemm_f32.hip).  Weight: hi/lo f16

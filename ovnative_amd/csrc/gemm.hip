@@ -328,6 +328,32 @@ __device__ __forceinline__ f32x4 mfma16(h8 a, h8 b) {
 }
 
 
+// rmsnorm_quantize of row r of a residual GEMM's result (kAccumNorm) from its
+// buffer resource: the row's values through L2 (sc1 loads), then the norm
+// and quantisation of rms_quant_row into a.nq / a.nsc.
+template <int P>
+__device__ __forceinline__ void norm_row_l2(__amdgpu_buffer_rsrc_t rs, const GemmArgs& a,
+                                            int64_t r, int lane, float* xt) {
+  constexpr int kSc1 = 16;  // cache policy bit SC1 (gfx940 family)
+  f32x4 xv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    xv[p] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (256 * p + 4 * lane) * 4, 0, kSc1));
+  rms_quant_row_vals<P>(xv, a.nw, a.neps, a.nq, a.nsc, r, a.n_tiled != 0, lane, xt);
+}
+
+// Workgroup id -> (n tile, m tile) with every n tile of an m tile on one XCD
+// (id % 8): XCD x takes m tiles x, x + 8, ..., each as n_tiles consecutive
+// slots; the grid has 8 n_tiles ceil(m_tiles / 8) workgroups, those past the
+// last m tile return at once.
+__device__ __forceinline__ bool band_tile_of(int id, int n_tiles, int m_tiles, int& nt, int& mt) {
+  const int xcd = id & 7, slot = id >> 3;
+  mt = xcd + 8 * (slot / n_tiles);
+  nt = slot % n_tiles;
+  return mt < m_tiles;
+}
+
 // NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.  PIPE:
 // the stage loop runs as a software pipeline (below); without it each stage
 // is read, multiplied and folded block by block.
@@ -373,7 +399,9 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   const int wn = wave % WN, wm = wave / WN;
   const int n_tiles = (a.N + BN - 1) / BN;
   int ntile, mtile;
-  if (!tile_of(wg, n_tiles, ntile, mtile)) return;  // padding workgroup
+  if (MODE == kAccumNorm ? !band_tile_of(wg, n_tiles, (a.M + BM - 1) / BM, ntile, mtile)
+                         : !tile_of(wg, n_tiles, ntile, mtile))
+    return;  // padding workgroup
   const int n0 = ntile * BN, m0 = mtile * BM;
   const int Kb = a.Kb;
   const int64_t Kp = a.Kp;
@@ -844,7 +872,7 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
       for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(f[i][j][e], ws[e]);
       if (lim >= 4 && ((uintptr_t)dst & 15u) == 0) {
         f32x4 v;
-        if (MODE == kAccumulate) {
+        if (MODE == kAccumulate || MODE == kAccumNorm) {
           const f32x4 c = *reinterpret_cast<const f32x4*>(dst);
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(o[e], c[e]);
@@ -856,7 +884,74 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (e < lim) dst[e] = MODE == kAccumulate ? __fadd_rn(o[e], dst[e]) : o[e];
+          if (e < lim)
+            dst[e] = (MODE == kAccumulate || MODE == kAccumNorm) ? __fadd_rn(o[e], dst[e]) : o[e];
+      }
+    }
+  }
+
+  if constexpr (MODE == kAccumNorm) {
+    // The band hand-off.  Once vmcnt has drained, this workgroup's result
+    // stores are in the XCD's L2, where the band's counter add is performed
+    // after them (atomics execute in L2; the counter's 256-byte line is this
+    // band's alone, so no other XCD holds it).
+    static_assert(BN == 32 && BM == 32, "bands of 32 rows, 32-column tiles");
+    static_assert(NW * kRmsRowLds<4> * 4 + 16 <= NST * STAGE, "the row norm's LDS fits in the ring");
+    wait_vm_lgkm<0>();
+    __syncthreads();  // every wavefront's stores drained; the ring is free
+    unsigned long long* const cnt = a.band_cnt + (int64_t)mtile * kBandCntStride;
+    unsigned long long* const bc = reinterpret_cast<unsigned long long*>(&smem[0][0]);
+    if (threadIdx.x == 0)
+      bc[0] = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const unsigned long long v = bc[0], nt = (unsigned long long)n_tiles;
+    const unsigned long long helpers = nt < kNormHelpers ? nt : kNormHelpers;
+    const unsigned long long arrived = v % nt;  // this launch's arrivals before this one
+    if (arrived < nt - helpers) return;
+    // Wait for the band's last arrival: agent-scope loads read the counter in
+    // L2.  At most kNormHelpers - 1 workgroups of a band wait, and only once
+    // their own tile is done: below 2048 rows that is at most 56 per XCD,
+    // fewer than its workgroup slots (32 CUs, several workgroups each), so the
+    // band's other workgroups can always run.  The wait is bounded all the
+    // same; one that runs out sets bit 2 of norm_err.
+    if (threadIdx.x == 0) {
+      const unsigned long long target = v - arrived + nt;
+      for (int it = 0; (long long)(__hip_atomic_load(cnt, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT) - target) < 0;
+           ++it) {
+        if (it == (1 << 18)) {
+          __hip_atomic_fetch_or(a.norm_err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    __syncthreads();
+    // helper h normalises rows h, h + helpers, ... of the band, one per
+    // wavefront.  The rows are read with sc1 loads, which go to L2: this CU's
+    // L1 may hold lines of them from before the other workgroups' stores (an
+    // L1 invalidate would do too, but buffer_inv sc1 also drops the XCD's
+    // clean L2 lines, which the band's neighbours are still reading).
+    const int h = (int)(arrived - (nt - helpers));
+    float* const xt = reinterpret_cast<float*>(&smem[0][0]) + wave * kRmsRowLds<4>;
+    for (int rr = h + (int)helpers * wave; rr < BM; rr += (int)helpers * NW) {
+      const int64_t r = m0 + rr;
+      if (r >= a.M) break;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          a.out[0] + r * a.ld[0], (short)0, a.N * 4, 0x00020000);
+      switch (a.N >> 8) {  // N = 256 P
+        case 1:
+          norm_row_l2<1>(rs, a, r, lane, xt);
+          break;
+        case 2:
+          norm_row_l2<2>(rs, a, r, lane, xt);
+          break;
+        case 3:
+          norm_row_l2<3>(rs, a, r, lane, xt);
+          break;
+        default:
+          norm_row_l2<4>(rs, a, r, lane, xt);
+          break;
       }
     }
   }
@@ -957,6 +1052,30 @@ hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
   return launch_qkv_cfg<32, true, false>(a, st);
 }
 
+// The residual GEMM followed by the row norm of its result (kAccumNorm):
+// 32 x 32 tiles, all of a 32-row band on one XCD.
+template <int WM, int SB, int NST>
+hipError_t launch_norm_cfg(const GemmArgs& a, hipStream_t st) {
+  if (a.Kb % SB) return hipErrorInvalidValue;
+  const int64_t n_tiles = ((int64_t)a.N + 31) / 32, m_tiles = ((int64_t)a.M + 31) / 32;
+  const dim3 grid((unsigned)(8 * n_tiles * ((m_tiles + 7) / 8))), block(128 * WM);
+  hipLaunchKernelGGL((gemm16_kernel<32, 32, 2, WM, SB, NST, kAccumNorm, true>), grid, block, 0, st,
+                     a);
+  return hipGetLastError();
+}
+
+// The tiles the residual mode takes below 2048 rows (launch_gemm).
+hipError_t launch_gemm_norm(const GemmArgs& a, hipStream_t st) {
+  if (a.Kb % 4 || a.nslices != 1 || !a.out[0] || !a.nw || !a.nq || !a.nsc || !a.band_cnt ||
+      !a.norm_err || a.N % 256 || a.N < 256 || a.N > 1024 || a.M >= 2048 || a.W16 || a.aq16)
+    return hipErrorInvalidValue;
+  const int64_t M = a.M;
+  if (M < 512 && a.Kb % 8 == 0) return launch_norm_cfg<2, 8, 3>(a, st);
+  if (M < 256) return launch_norm_cfg<2, 4, 3>(a, st);
+  if (M < 1024) return a.Kb % 8 == 0 ? launch_norm_cfg<2, 8, 2>(a, st) : launch_norm_cfg<2, 4, 3>(a, st);
+  return launch_norm_cfg<1, 4, 2>(a, st);
+}
+
 template <int BN, int BM, int WN, int WM, int SB>
 hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
@@ -973,6 +1092,7 @@ hipError_t launch_cfg_sb(const GemmArgs& a, GemmMode mode, hipStream_t st) {
       break;
     case kSiluQuant:  // the 16x16 kernel's modes only
     case kQkvNorm:
+    case kAccumNorm:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1059,6 +1179,7 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // (the LM step, whose weights come cold from HBM) the 256x64 tile of 8
   // wavefronts: 16.0 against 17.4 us with cold weights.
   if (mode == kQkvNorm) return launch_qkv_norm(a, st);
+  if (mode == kAccumNorm) return launch_gemm_norm(a, st);
   if ((a.W16 != nullptr) != (a.aq16 != nullptr)) return hipErrorInvalidValue;
   if (a.W16) {
     // f16 form (sweep at M = 16384, N = 1024..8200, K = 1024..3072, MI355X):

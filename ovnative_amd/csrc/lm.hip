@@ -350,6 +350,12 @@ struct OvhLm {
   std::vector<int64_t> graph_key;
   hipStream_t own_st = nullptr;
   uint32_t* d_overflow = nullptr;
+  // o_proj and down with the following RMSNorm + quantise in the same launch
+  // (GemmMode kAccumNorm) where the layout allows it; their band counters
+  // (zeroed when allocated, then only advanced by the launches)
+  bool norm_fused = true;
+  unsigned long long* d_band = nullptr;
+  int64_t band_words = 0;
   // RoPE tables of the last position list (rebuilt only when it changes)
   std::vector<int64_t> tab_pos;
   std::vector<float> tab_host;
@@ -373,6 +379,7 @@ struct OvhLm {
     if (h_out) (void)hipHostFree(h_out);
     if (d_tab) (void)hipFree(d_tab);
     if (d_overflow) (void)hipFree(d_overflow);
+    if (d_band) (void)hipFree(d_band);
     if (graph) (void)hipGraphExecDestroy(graph);
     if (own_st) (void)hipStreamDestroy(own_st);
   }
@@ -651,6 +658,21 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
       f16 = ovh::weight_f16(Y.qkv, L.st) && ovh::weight_f16(Y.o, L.st) &&
             ovh::weight_f16(Y.gate_up, L.st) && ovh::weight_f16(Y.down, L.st);
   if (f16 && !L.head->f32) f16 = ovh::weight_f16(L.head, L.st);
+  // the residual GEMMs' fused norm: tile-major codes, the int8 form, the
+  // 32-row residual tiles (below 2048 rows)
+  const bool nfuse = L.norm_fused && tiled && !f16 && T < 2048;
+  if (nfuse && ovh::band_counter_words(T) > L.band_words) {
+    // before any capture; the old counters may still be in use by the stream
+    OVH_HIP(hipStreamSynchronize(L.st), "hipStreamSynchronize");
+    if (L.d_band) OVH_HIP(hipFree(L.d_band), "hipFree(band counters)");
+    L.d_band = nullptr;
+    L.band_words = 0;
+    const int64_t words = ovh::band_counter_words(2048);
+    OVH_HIP(hipMalloc(reinterpret_cast<void**>(&L.d_band), sizeof(unsigned long long) * words),
+            "hipMalloc(band counters)");
+    OVH_HIP(hipMemset(L.d_band, 0, sizeof(unsigned long long) * words), "hipMemset(band counters)");
+    L.band_words = words;
+  }
   std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
   int64_t bias_elems = 0, bits_words = 0;
   for (size_t i = 0; i < segs.size(); ++i) {
@@ -692,6 +714,10 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
             b_g = take(sizeof(float) * (size_t)(Tpad * I)),  // also the SiLU codes, Tpad rows
             b_u = take(sizeof(float) * (size_t)(T * I)),
             b_lg = take(sizeof(float) * (size_t)(T * CV));
+  // the post-attention norm's codes when o_proj writes them (its own operand,
+  // the attention's codes, is still being read by the other bands)
+  const Buf b_aq2 = take(nfuse ? (size_t)(Tpad * H) : 0),
+            b_asc2 = take(nfuse ? sizeof(float) * (size_t)(T * (H / 32)) : 0);
   // fp32 head: the final norm's output as f16 hi/lo planes and row scales
   const bool head_f32 = L.head->f32;
   const size_t hplane = head_f32 ? sizeof(_Float16) * (size_t)ovh::f32_plane_halves(T, H) : 0;
@@ -734,6 +760,8 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   float* up = static_cast<float*>(at(b_u));
   float* logits = static_cast<float*>(at(b_lg));
   _Float16* aq16 = f16 ? static_cast<_Float16*>(at(b_aq16)) : nullptr;
+  int8_t* aq2 = static_cast<int8_t*>(at(b_aq2));
+  float* asc2 = static_cast<float*>(at(b_asc2));
   hipStream_t st = L.st;
 
   // stage the inputs in pinned memory (after the previous upload has left it)
@@ -861,8 +889,10 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     float* qkv_c[3] = {q, k, v};
     const int64_t gu_n[2] = {I, I};
     float* gu_c[2] = {gate, up};
-    for (const OvhLm::Layer& Y : L.layers) {
-      if ((rc = norm_q(Y.ln1)) != OV_OK) return rc;
+    for (size_t li = 0; li < L.layers.size(); ++li) {
+      const OvhLm::Layer& Y = L.layers[li];
+      // with nfuse, the previous layer's down launch normalised x into aq/asc
+      if ((li == 0 || !nfuse) && (rc = norm_q(Y.ln1)) != OV_OK) return rc;
       if (qkv_fused) {
         // q/k/v GEMM + qk-norm/RoPE + K/V planes in one launch, then attention
         ovh::GemmArgs ga;
@@ -903,8 +933,22 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           return rc;
       }
       if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
-      if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled, aq16, f16)) != OV_OK) return rc;
-      if ((rc = norm_q(Y.ln2)) != OV_OK) return rc;
+      // x += o_proj(attention), then the post-attention norm's codes: in one
+      // launch into aq2/asc2, or a second launch into aq/asc
+      const int8_t* naq = nfuse ? aq2 : aq;
+      const float* nasc = nfuse ? asc2 : asc;
+      if (nfuse) {
+        if ((rc = ovh::linear_q_norm(T, aq, asc, Y.o, x, H, Y.ln2, c.rms_eps, aq2, asc2, L.d_band,
+                                     L.d_overflow, st)) != OV_OK)
+          return rc;
+      } else {
+        if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled, aq16, f16)) != OV_OK) return rc;
+        if ((rc = norm_q(Y.ln2)) != OV_OK) return rc;
+      }
+      // the norm after down: the next layer's input norm, or the final norm of
+      // an int8 head
+      const bool last = li + 1 == L.layers.size();
+      const float* next_ln = last ? (head_f32 ? nullptr : L.final_norm) : L.layers[li + 1].ln1;
       if (L.silu_fused) {
         // h = silu(gate) * up, quantised, straight from the gate/up GEMM into the
         // (otherwise unused) gate/up buffers: codes [T][I], scales [T][I/32]
@@ -913,8 +957,8 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         ga.N = (int)(2 * I);
         ga.Kb = (int)ovh::kb_of(H);
         ga.Kp = 32 * ovh::kb_of(H);
-        ga.aq = aq;
-        ga.asc = asc;
+        ga.aq = naq;
+        ga.asc = nasc;
         ga.W = Y.gate_up->w.q;
         ga.ws = Y.gate_up->w.scale;
         ga.hq = reinterpret_cast<int8_t*>(gate);
@@ -928,8 +972,14 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           ga.aq16 = aq16;
         }
         OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
-        if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled, aq16, f16)) != OV_OK)
+        if (nfuse && next_ln) {
+          if ((rc = ovh::linear_q_norm(T, ga.hq, ga.hsc, Y.down, x, H, next_ln, c.rms_eps, aq, asc,
+                                       L.d_band, L.d_overflow, st)) != OV_OK)
+            return rc;
+        } else if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled, aq16, f16)) !=
+                   OV_OK) {
           return rc;
+        }
       } else {
         if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
         if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
@@ -959,8 +1009,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
       OVH_HIP(ovh::launch_gemm_f32(ha, st), "fp32 head launch");
       return OV_OK;
     }
-    if ((rc = norm_q(L.final_norm)) != OV_OK)
-      return rc;
+    if (!nfuse && (rc = norm_q(L.final_norm)) != OV_OK) return rc;
     return ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled, aq16, f16);
   };
 
@@ -971,7 +1020,8 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     // and every buffer address the launches take.  A changed layout (other
     // lengths, a grown arena, new RoPE tables) is captured anew; the same
     // layout replays over the new inputs the upload above brought.
-    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, f16, (int64_t)segs.size(),
+    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, f16, nfuse,
+                                (int64_t)(intptr_t)L.d_band, (int64_t)segs.size(),
                                 (int64_t)in_bytes, (int64_t)(intptr_t)L.arena,
                                 (int64_t)(intptr_t)cosb, (int64_t)(intptr_t)sinb};
     for (size_t i = 0; i < segs.size(); ++i) {
@@ -1013,6 +1063,10 @@ int check_overflow(OvhLm& L) {
   if (!flag) return OV_OK;
   const uint32_t zero = 0;
   OVH_HIP(hipMemcpy(L.d_overflow, &zero, sizeof zero, hipMemcpyHostToDevice), "clear overflow flag");
+  if (flag & 2u)
+    return set_error(OV_ERR_INTERNAL, "residual GEMM + norm: a band hand-off wait ran out (the "
+                                      "band's workgroups did not all run): switch to "
+                                      "ovh_lm_set_fused_norm(lm, 0)");
   return set_error(OV_ERR_INTERNAL, "attention inputs beyond the f16 range for the split-f16 "
                                     "kernel: switch to ovh_lm_set_attention(lm, 0)");
 }
@@ -1141,6 +1195,10 @@ void ovh_lm_set_attention(OvhLm* lm, int split_f16) {
 
 void ovh_lm_set_graphs(OvhLm* lm, int on) {
   if (lm) lm->use_graphs = on != 0;
+}
+
+void ovh_lm_set_fused_norm(OvhLm* lm, int on) {
+  if (lm) lm->norm_fused = on != 0;
 }
 
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

@@ -105,15 +105,15 @@ __device__ __forceinline__ float quant_block_lane(const float v[4], int nvalid, 
 // 0..7 stream their chains with ds_read_b128; the 8 chains are added in order.
 template <int P>
 constexpr int kRmsRowLds = 8 * (32 * P + 4);
+// rms_quant_row_vals takes the row's values already loaded (xv[p] = elements
+// 256p + 4l..+3).
 template <int P>
-__device__ __forceinline__ void rms_quant_row(const float* __restrict__ row,
-                                              const float* __restrict__ w, float eps,
-                                              int8_t* __restrict__ aq, float* __restrict__ asc,
-                                              int64_t r, bool tiled, int lane, float* xt) {
+__device__ __forceinline__ void rms_quant_row_vals(const f32x4 (&xv)[P], const float* __restrict__ w,
+                                                   float eps, int8_t* __restrict__ aq,
+                                                   float* __restrict__ asc, int64_t r, bool tiled,
+                                                   int lane, float* xt) {
   constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
-  f32x4 xv[P], wv[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) xv[p] = *reinterpret_cast<const f32x4*>(row + 256 * p + 4 * lane);
+  f32x4 wv[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
   // element 256p + 4l + c -> chain 4(l&1) + c, position 32p + l/2
@@ -151,6 +151,17 @@ __device__ __forceinline__ void rms_quant_row(const float* __restrict__ row,
     *reinterpret_cast<uint32_t*>(aq + act_index(r, 256 * p + 4 * lane, cols, tiled)) = codes;
     if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
   }
+}
+
+template <int P>
+__device__ __forceinline__ void rms_quant_row(const float* __restrict__ row,
+                                              const float* __restrict__ w, float eps,
+                                              int8_t* __restrict__ aq, float* __restrict__ asc,
+                                              int64_t r, bool tiled, int lane, float* xt) {
+  f32x4 xv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) xv[p] = *reinterpret_cast<const f32x4*>(row + 256 * p + 4 * lane);
+  rms_quant_row_vals<P>(xv, w, eps, aq, asc, r, tiled, lane, xt);
 }
 
 // silu(g) * u as the reference's exp256 lanes compute it (ops_cpu.cpp:75-92,

@@ -431,6 +431,32 @@ def test_graph_replays_match_eager(small_lm):
     assert np.array_equal(got, eager)
 
 
+@pytest.mark.parametrize("batch,seq", [(1, 37), (2, 64), (2, 300), (2, 660)])
+def test_fused_norm_equals_separate_norm(small_lm, batch, seq):
+    """o_proj and down with the RMSNorm + quantise that follows each of them in
+    the same launch (the default below 2048 rows: the last workgroups to finish
+    each 32-row band normalise its rows) give the bits of the norm as a launch
+    of its own, over graph replays and eager launches alike: a partial last
+    band (37 rows), the 4-wavefront tiles (128 and 600 rows) and the
+    2-wavefront tiles (1320 rows)."""
+    ts, table, lm = small_lm
+    x = make_inputs(41 + seq, SMALL, batch, seq, min(12, seq // 3))
+    lm.set_fused_norm(False)
+    try:
+        want = lm.forward(*x)
+    finally:
+        lm.set_fused_norm(True)
+    for rep in range(3):
+        got = lm.forward(*x)
+        assert np.array_equal(got.view(np.int32), want.view(np.int32)), rep
+    lm.set_graphs(False)
+    try:
+        got = lm.forward(*x)
+    finally:
+        lm.set_graphs(True)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))
+
+
 # ---------------------------------------------------------------------------
 # BASELINE config 4 at full size: 28 layers, hidden 1024, 16/8 heads, inter
 # 3072, head 8 x 1025, the tts.cpp CFG batch B = 2, S = 300 (40 text + 260
