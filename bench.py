@@ -70,6 +70,9 @@ def attention_flops(cfg: dict, seq: int, batch: int, layers: int) -> int:
     return layers * batch * cfg["n_heads"] * 4 * seq * seq * cfg["head_dim"]
 
 
+NORM_TRAFFIC = "gemm_residual_norm_m600_traffic.json"
+
+
 def residual_traffic(name="gemm_residual_m600_traffic.json"):
     """HBM bytes per launch of the residual GEMM (mean of the o_proj and down
     launches), or of the kernel another committed PMC summary names (FETCH_SIZE
@@ -215,6 +218,15 @@ def residual_bytes(cfg: dict, M: int) -> float:
     return (one(QD) + one(I)) / 2
 
 
+def norm_out_bytes(cfg: dict, M: int) -> float:
+    """Algorithmic HBM bytes the fused RMSNorm + quantise adds to a residual
+    launch: its codes M*N and fp32 block scales 4*M*N/32 written, its weight 4N
+    read (the updated rows it normalises are the launch's own output, read back
+    from L2)."""
+    H = cfg["hidden"]
+    return M * H + 4 * M * (H // 32) + 4 * H
+
+
 # Epilogue ceiling of the int8 GEMM with the reference's exact epilogue: per
 # output and 32-k block one v_cvt_f32_i32 and one v_fma_f32; a wave64 VALU
 # instruction takes 4 clocks on a 16-lane SIMD, so a 16x16x32 block product
@@ -245,7 +257,8 @@ def roofline_entry(kernel: str, ops: float, nbytes: float, ms: float, traffic=No
     return e
 
 
-def time_residual(cfg: dict, layers: int, M: int, reps: int = 4, eager: bool = True):
+def time_residual(cfg: dict, layers: int, M: int, reps: int = 4, eager: bool = True,
+                  norm: bool = False):
     """The residual GEMM as the step runs it: `layers` o_proj (K = heads*128) and
     `layers` down (K = inter) launches on distinct weights with tile-major codes
     (the runner's layout), accumulating into one fp32 [M, hidden] buffer,
@@ -255,8 +268,12 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4, eager: bool = T
     as in the step, where 440 MB of weights go by between two uses of one
     weight, every launch reads its weight from HBM rather than from the 256 MB
     last-level cache.  Also timed: the same launches eagerly through the C ABI
-    with row-major codes.  Returns dict(graph_ms, eager_ms per launch, ops per
-    launch on average)."""
+    with row-major codes.  With `norm`, the same launches as the step makes them
+    below 2048 rows, each with the RMSNorm + quantise that follows it
+    (ovh_linear_q_norm: o_proj with the post-attention norm, down with the next
+    layer's input norm), captured and replayed the same way.  Returns
+    dict(graph_ms, eager_ms, graph_norm_ms per launch, ops per launch on
+    average)."""
     import torch
     import ovnative_amd as ov
     H, QD, I = cfg["hidden"], cfg["n_heads"] * cfg["head_dim"], cfg["inter"]
@@ -313,6 +330,38 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4, eager: bool = T
     torch.cuda.synchronize()
     out["graph_ms"] = e0.elapsed_time(e1) / n
     del graph
+    if norm:
+        nw = [torch.rand(H, generator=g, device="cuda") + 0.5 for _ in range(2)]
+        nq = torch.zeros(lib.ovh_tiled_codes_bytes(M, H), dtype=torch.int8, device="cuda")
+        nsc = torch.empty((M, H // 32), device="cuda")
+        cnt = ov.band_counters()
+
+        def launches_norm(st):
+            for a, b in zip(wo, wd):
+                for (t, sc, w, v) in ((to, ao[1], a, nw[0]), (td, ad[1], b, nw[1])):
+                    if lib.ovh_linear_q_norm(M, t.data_ptr(), sc.data_ptr(), w.handle,
+                                             x.data_ptr(), H, v.data_ptr(), cfg["rms_eps"],
+                                             nq.data_ptr(), nsc.data_ptr(), cnt.data_ptr(),
+                                             st) != 0:
+                        raise RuntimeError(ov.load().ovh_last_error().decode())
+        graph = torch.cuda.CUDAGraph()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            launches_norm(side.cuda_stream)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            launches_norm(torch.cuda.current_stream().cuda_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out["graph_norm_ms"] = e0.elapsed_time(e1) / n
+        if int(cnt[0].item()) != 0:
+            raise RuntimeError("residual + norm: a band hand-off wait ran out")
+        del graph
     for w in wo + wd:
         w.free()
     return out
@@ -329,12 +378,18 @@ def run_residual(args) -> None:
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    rs = time_residual(CFG, args.layers, M, eager=False)
+    rs = time_residual(CFG, args.layers, M, eager=False, norm=True)
     nbytes = residual_bytes(CFG, M)
-    print(json.dumps({"workload": "residual GEMM roofline kernel (o_proj and down, M=600, "
-                                  "weights cold, graph replay) + 64 MiB copy calibration",
-                      "roofline": roofline_entry("gemm16 residual", rs["ops"], nbytes,
-                                                 rs["graph_ms"], residual_traffic())}),
+    print(json.dumps({"workload": "the residual GEMM launches of the step (o_proj and down, "
+                                  "M=600, weights cold, graph replay), plain and with the "
+                                  "following RMSNorm + quantise (the roofline kernel), after a "
+                                  "64 MiB copy calibration",
+                      "roofline": roofline_entry("gemm16 residual + norm", rs["ops"],
+                                                 nbytes + norm_out_bytes(CFG, M),
+                                                 rs["graph_norm_ms"],
+                                                 residual_traffic(NORM_TRAFFIC)),
+                      "plain_residual": roofline_entry("gemm16 residual", rs["ops"], nbytes,
+                                                       rs["graph_ms"], residual_traffic())}),
           flush=True)
 
 
@@ -962,7 +1017,7 @@ def main():
     gen_ms = (time.perf_counter() - t_gen) * 1e3
     log(f"32-step decode {gen_ms:.1f} ms")
 
-    rs = time_residual(cfg, args.layers, M)
+    rs = time_residual(cfg, args.layers, M, norm=True)
     step.lm.close()
 
     cpu = None if args.no_cpu else cpu_baseline(cfg, tensors, args.cpu_seconds)
@@ -995,10 +1050,13 @@ def main():
             "lm_32_steps_note": "ovh_lm_generate wall clock: 32 forwards + device sampling + host top-k",
         },
         "roofline": roofline_entry(
-            "gemm16 residual (o_proj K=2048 and down K=3072; M=600, N=1024, += x), launched "
-            "as the step launches it: graph replay, tile-major codes, weights cold from HBM",
-            rs["ops"], residual_bytes(cfg, M), rs["graph_ms"], residual_traffic(),
-            avg_ms_eager_rowmajor=round(rs["eager_ms"], 5)),
+            "gemm16 residual + norm (o_proj K=2048 and down K=3072; M=600, N=1024, += x, then "
+            "RMSNorm + quantise of the updated rows in the same launch), launched as the step "
+            "launches it: graph replay, tile-major codes, weights cold from HBM",
+            rs["ops"], residual_bytes(cfg, M) + norm_out_bytes(cfg, M), rs["graph_norm_ms"],
+            residual_traffic(NORM_TRAFFIC),
+            avg_ms_plain_residual=round(rs["graph_ms"], 5),
+            avg_ms_plain_residual_eager_rowmajor=round(rs["eager_ms"], 5)),
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }

@@ -47,6 +47,8 @@ SIGNATURES = {
     "ovh_linear_q": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
     "ovh_linear_q_tiled": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
+    "ovh_linear_q_norm": (_int, [_i64, _p, _p, _p, _p, _i64, _p, _f32, _p, _p, _p, _p]),
+    "ovh_band_counter_bytes": (_i64, []),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_noalloc": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_weight_upload_f32": (_int, [_i64, _i64, _p, _int, _p, C.POINTER(_p)]),
@@ -333,6 +335,27 @@ def linear_q_tiled(aq_tiled, asc, w: Weight, M: int, C=None, accumulate: bool = 
     _check(load().ovh_linear_q_tiled(M, _dptr(aq_tiled), _dptr(asc), w.handle, _dptr(C),
                                      C.shape[1], int(bool(accumulate)), _stream()))
     return C
+
+
+def band_counters():
+    """Zeroed device memory for linear_q_norm's band counters: allocate one per
+    device and output width N, and pass it to every call (stream-ordered)."""
+    torch = _torch()
+    return torch.zeros(load().ovh_band_counter_bytes() // 8, dtype=torch.int64, device="cuda")
+
+
+def linear_q_norm(aq_tiled, asc, w: Weight, x, nw, band_cnt, eps: float = 1e-6):
+    """x[M, N] += linear_q_tiled(aq_tiled, asc, w), then rmsnorm_quantize of the
+    updated rows with weight nw, in one launch (lm.cpp:281 + :292, :311 + :232).
+    Returns (codes tile-major, zero past row M; scales [M, N / 32])."""
+    torch = _torch()
+    M, N = x.shape
+    nq = torch.zeros(load().ovh_tiled_codes_bytes(M, N), dtype=torch.int8, device="cuda")
+    nsc = torch.empty((M, N // 32), dtype=torch.float32, device="cuda")
+    _check(load().ovh_linear_q_norm(M, _dptr(aq_tiled), _dptr(asc), w.handle, _dptr(x), N,
+                                    _dptr(nw), eps, _dptr(nq), _dptr(nsc), _dptr(band_cnt),
+                                    _stream()))
+    return nq, nsc
 
 
 class GemmGroup(C.Structure):

@@ -544,6 +544,28 @@ int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhW
   return ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), true);
 }
 
+// band_cnt: the hand-off error word in the first counter slot, then one slot
+// per 32-row band (band_counter_words(2048): every M the entry point takes)
+int64_t ovh_band_counter_bytes(void) {
+  return (int64_t)sizeof(unsigned long long) * (ovh::kBandCntStride + ovh::band_counter_words(2048));
+}
+
+int ovh_linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
+                      int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
+                      void* band_cnt, void* stream) {
+  if (M <= 0) return OV_OK;
+  if (!w) return fail(OV_ERR_INVALID_ARG, "weight is null");
+  if (M >= 2048) return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_norm: M must be below 2048");
+  if (w->w.Kb % 4 != 0)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_norm: K must be a multiple of 128");
+  if (w->w.N % 256 != 0 || w->w.N > 1024)
+    return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_norm: N must be 256, 512, 768 or 1024");
+  if (!band_cnt) return fail(OV_ERR_INVALID_ARG, "band_cnt is null");
+  auto* cnt = static_cast<unsigned long long*>(band_cnt);
+  return ovh::linear_q_norm(M, aq, asc, w, x, ldx, nw, eps, nq, nsc, cnt + ovh::kBandCntStride,
+                            reinterpret_cast<uint32_t*>(cnt), as_stream(stream));
+}
+
 int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w,
                         const int64_t* slice_n, float* const* slice_c, int n_slices,
                         void* stream) {

@@ -24,10 +24,11 @@ enum GemmMode {
 // rmsnorm_quantize of the rows it updated.  Each 32-row tile of the output (a
 // band) is computed by workgroups of one XCD; each counts itself in its
 // band's counter once its stores are in that XCD's L2, and the last
-// kNormHelpers to arrive wait for the count to complete and normalise the
-// band's rows.  The counters are 64-bit, kBandCntStride words apart, zero
-// when allocated, and advance by the number of column tiles per launch.
-constexpr int kNormHelpers = 8;
+// GemmArgs::n_helpers to arrive (the launcher picks up to kMaxNormHelpers)
+// wait for the count to complete and normalise the band's rows.  The
+// counters are 64-bit, kBandCntStride words apart, zero when allocated, and
+// advance by the number of column tiles per launch.
+constexpr int kMaxNormHelpers = 32;
 constexpr int kBandCntStride = 32;
 // 64-bit words of band counters for M rows
 inline int64_t band_counter_words(int64_t M) { return (M + 31) / 32 * kBandCntStride; }
@@ -106,6 +107,7 @@ struct GemmArgs {
   int n_tiled = 0;
   unsigned long long* band_cnt = nullptr;
   uint32_t* norm_err = nullptr;
+  int n_helpers = 8;  // set by the launcher
 };
 
 // fp32 linear on the f16 matrix cores (gemm_f32.hip).  Weight: hi/lo f16

@@ -905,15 +905,16 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
       bc[0] = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const unsigned long long v = bc[0], nt = (unsigned long long)n_tiles;
-    const unsigned long long helpers = nt < kNormHelpers ? nt : kNormHelpers;
+    const unsigned long long helpers =
+        nt < (unsigned long long)a.n_helpers ? nt : (unsigned long long)a.n_helpers;
     const unsigned long long arrived = v % nt;  // this launch's arrivals before this one
     if (arrived < nt - helpers) return;
     // Wait for the band's last arrival: agent-scope loads read the counter in
-    // L2.  At most kNormHelpers - 1 workgroups of a band wait, and only once
-    // their own tile is done: below 2048 rows that is at most 56 per XCD,
-    // fewer than its workgroup slots (32 CUs, several workgroups each), so the
-    // band's other workgroups can always run.  The wait is bounded all the
-    // same; one that runs out sets bit 2 of norm_err.
+    // L2.  At most n_helpers - 1 workgroups of a band wait, and only once
+    // their own tile is done; the launcher keeps their number over the
+    // XCD's bands below its workgroup slots, so the bands' other workgroups
+    // can always run.  The wait is bounded all the same; one that runs out
+    // sets bit 2 of norm_err.
     if (threadIdx.x == 0) {
       const unsigned long long target = v - arrived + nt;
       for (int it = 0; (long long)(__hip_atomic_load(cnt, __ATOMIC_RELAXED,
@@ -1054,13 +1055,42 @@ hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
 
 // The residual GEMM followed by the row norm of its result (kAccumNorm):
 // 32 x 32 tiles, all of a 32-row band on one XCD.
+// Helpers per band: as many as the waiting ones leave the bands' other
+// workgroups room.  A band's waiting workgroups (helpers - 1 at most) hold
+// their slots until the band completes; over the bands one XCD holds at once
+// (all of its bands, at worst) they must stay below the XCD's workgroup slots
+// (resident workgroups per CU x CUs per XCD, 32 on MI355X), so that every
+// band's remaining workgroups can still be dispatched.  Measured at M = 600
+// (LM step, 19 bands): 32 helpers (one row each) 2.307 ms, 16 2.311, 8 2.34,
+// 4 2.49: the more CUs share a band's rows, the shorter the launch's tail.
+int norm_helpers(int occ, int64_t bands) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0 || occ <= 0)
+    return 1;
+  const int xcds = cus >= 64 ? cus / 32 : 1;
+  const int64_t per_xcd = (bands + xcds - 1) / xcds, slots = (int64_t)occ * (cus / xcds);
+  int h = kMaxNormHelpers;
+  while (h > 1 && (int64_t)(h - 1) * per_xcd >= slots) h /= 2;
+  return h;
+}
+
 template <int WM, int SB, int NST>
 hipError_t launch_norm_cfg(const GemmArgs& a, hipStream_t st) {
   if (a.Kb % SB) return hipErrorInvalidValue;
   const int64_t n_tiles = ((int64_t)a.N + 31) / 32, m_tiles = ((int64_t)a.M + 31) / 32;
   const dim3 grid((unsigned)(8 * n_tiles * ((m_tiles + 7) / 8))), block(128 * WM);
-  hipLaunchKernelGGL((gemm16_kernel<32, 32, 2, WM, SB, NST, kAccumNorm, true>), grid, block, 0, st,
-                     a);
+  auto kernel = gemm16_kernel<32, 32, 2, WM, SB, NST, kAccumNorm, true>;
+  // resident workgroups per CU: a property of this kernel on the architecture
+  static const int occ = [&] {
+    int o = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 128 * WM, 0) == hipSuccess ? o
+                                                                                              : 0;
+  }();
+  GemmArgs b = a;
+  b.n_helpers = norm_helpers(occ, m_tiles);
+  hipLaunchKernelGGL(kernel, grid, block, 0, st, b);
   return hipGetLastError();
 }
 

@@ -636,6 +636,60 @@ def test_linear_q_tiled_equals_rowmajor(oracle, M, N, K):
     assert np.array_equal(bits(host(c1)), bits(host(c2)))
 
 
+@pytest.mark.parametrize("M,N,K", [(600, 1024, 2048), (600, 1024, 3072), (128, 1024, 3072),
+                                   (1, 1024, 2048), (37, 256, 512), (300, 512, 1024),
+                                   (1320, 1024, 2048), (2047, 768, 1024)])
+def test_linear_q_norm_equals_two_calls(oracle, M, N, K):
+    """ovh_linear_q_norm (the runner's o_proj / down launch, with the RMSNorm +
+    quantise that follows it: lm.cpp:281 + :292, :311 + :232) gives the bits of
+    ovh_linear_q_tiled in its residual form followed by ovh_rmsnorm_quantize,
+    codes tile-major, over repeated calls on one counter buffer; the norm's
+    codes and scales are also the oracle's rmsnorm_quantize of the updated
+    rows."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(7 * M + N + K)
+    A, Wf = _rand_problem(rng, M, N, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    t = ov.tile_major(aq)
+    nw_h = rng.uniform(0.1, 1.1, N).astype(np.float32)
+    nw = dev(nw_h)
+    cnt = ov.band_counters()
+    Cin = rng.standard_normal((M, N)).astype(np.float32)
+    want_x = dev(Cin)
+    ov.linear_q_tiled(t, asc, w, M, want_x, accumulate=True)
+    want_q, want_s = ov.rmsnorm_quantize(want_x, nw, 1e-6)
+    aq_r, asc_r = oracle.rmsnorm_quantize(host(want_x), nw_h, 1e-6)
+    assert np.array_equal(host(want_q), u8_to_s8(aq_r, N))
+    assert np.array_equal(bits(host(want_s)), bits(asc_r))
+    for rep in range(3):
+        x = dev(Cin)
+        nq, nsc = ov.linear_q_norm(t, asc, w, x, nw, cnt, 1e-6)
+        assert np.array_equal(bits(host(x)), bits(host(want_x))), rep
+        assert np.array_equal(host(nq), tile_major(host(want_q), M)), rep
+        assert np.array_equal(bits(host(nsc)), bits(host(want_s))), rep
+    assert host(cnt)[0] == 0  # no hand-off wait ran out
+
+
+def test_linear_q_norm_errors(oracle):
+    import ovnative_amd as ov
+    q, s = oracle.quantize_weight_rows(np.ones((1024, 1100), np.float32) * 0.01)
+    w = ov.Weight.from_host(q, s)          # K = 1100: 35 blocks, not a multiple of 4
+    aq, asc = ov.s8_nk_quantize(dev(np.ones((4, 1100), np.float32)))
+    x = dev(np.zeros((4, 1024), np.float32))
+    nw = dev(np.ones(1024, np.float32))
+    cnt = ov.band_counters()
+    with pytest.raises(ov.OvhError, match="multiple of 128"):
+        ov.linear_q_norm(ov.tile_major(aq), asc, w, x, nw, cnt)
+    q, s = oracle.quantize_weight_rows(np.ones((320, 1024), np.float32) * 0.01)
+    w = ov.Weight.from_host(q, s)          # N = 320
+    aq, asc = ov.s8_nk_quantize(dev(np.ones((4, 1024), np.float32)))
+    with pytest.raises(ov.OvhError, match="N must be"):
+        ov.linear_q_norm(ov.tile_major(aq), asc, w, dev(np.zeros((4, 320), np.float32)),
+                         dev(np.ones(320, np.float32)), cnt)
+
+
 @pytest.mark.parametrize("M", [1, 100, 128, 256, 600, 2400])
 def test_silu_gate_linear_vs_oracle(oracle, M):
     """ovh_silu_gate_linear (gate/up GEMM with silu*up and its quantisation in the
