@@ -818,7 +818,7 @@ def run_layer(args) -> None:
     tops = layer_ops / (layer_ms * 1e-3) / 1e12
     log(f"config 3: forward 1 layer {ms[1]:.3f} ms, 2 layers {ms[2]:.3f} ms -> layer "
         f"{layer_ms * 1e3:.1f} us ({tops:.1f} linear TOPS)")
-    rs = time_residual(CFG, 1, M, reps=16)
+    rs = time_residual(CFG, 1, M, reps=16, norm=True)
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -857,16 +857,19 @@ def run_layer(args) -> None:
         args, round(tops, 2), "TOPS", round(layer_ms, 5),
         {"workload": (f"BASELINE config 3: one Qwen3-0.6B-shaped decoder layer at M=2x{SEQ} (the "
                       "config-4 CFG batch): RMSNorm+quant, merged q/k/v, qk-norm+RoPE, GQA "
-                      "attention (split-f16), o_proj (+= x), RMSNorm+quant, gate/up+SiLU, down "
-                      "(+= x); runner forward at 2 layers minus 1 layer"),
+                      "attention (split-f16), o_proj (+= x) with the next RMSNorm+quant in the "
+                      "same launch, gate/up+SiLU, down (+= x) with the next layer's "
+                      "RMSNorm+quant; runner forward at 2 layers minus 1 layer"),
          "model": "one decoder layer (hidden 1024, 16/8 heads x 128, inter 3072)",
          "global_batch": CFG_BATCH, "seq_len": SEQ, "parallelism": "single GPU",
          "layer_linear_gop": round(layer_ops / 1e9, 3),
          "forward_1_layer_ms": round(ms[1], 4), "forward_2_layers_ms": round(ms[2], 4)},
-        roofline_entry(f"gemm16 residual (o_proj K=2048 and down K=3072; M={M}, N=1024, += x; "
+        roofline_entry(f"gemm16 residual + norm (o_proj K=2048 and down K=3072; M={M}, N=1024, "
+                       "+= x, then RMSNorm + quantise of the updated rows in the same launch; "
                        "one layer's weights, cache-hot as in this workload; graph replay, "
-                       "tile-major codes)", rs["ops"], residual_bytes(CFG, M), rs["graph_ms"],
-                       avg_ms_eager_rowmajor=round(rs["eager_ms"], 5)),
+                       "tile-major codes)", rs["ops"], residual_bytes(CFG, M) + norm_out_bytes(CFG, M),
+                       rs["graph_norm_ms"], avg_ms_plain_residual=round(rs["graph_ms"], 5),
+                       avg_ms_plain_residual_eager_rowmajor=round(rs["eager_ms"], 5)),
         cpu, round(wall, 3))
     print(json.dumps(line), flush=True)
 

@@ -84,13 +84,22 @@ struct MaskJobs {
   MaskJob job[kAttnMaxSegs];
 };
 constexpr int kEmbMaxC = 16;  // codebooks the vector path holds in registers
+// The first layer's input norm in the embedding launch (rmsnorm_quantize of
+// each embedded row, tile-major codes): w null = off.  Vector path, H = 256 P
+// with P <= 4.
+struct EmbNorm {
+  const float* w;
+  float eps;
+  int8_t* aq;
+  float* asc;
+};
 
 __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ ids,
                                                     const uint8_t* __restrict__ mask, int seq,
                                                     int C, int64_t H, EmbTable tok, EmbTable aud,
                                                     const int64_t* __restrict__ offsets,
                                                     float* __restrict__ out, int64_t T,
-                                                    MaskJobs mj) {
+                                                    MaskJobs mj, EmbNorm nrm) {
   const int64_t wg = blockIdx.x;
   if (wg >= T) {
     const int64_t mw = wg - T;
@@ -135,6 +144,29 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
       const int64_t id = ids[b * C * seq + s];
       for (int64_t h = 4 * (int64_t)threadIdx.x; h < H; h += 4 * (int64_t)blockDim.x)
         *reinterpret_cast<f32x4*>(o + h) = emb4(tok, id, H, h);
+    }
+    if (nrm.w) {
+      // the workgroup's stores of the row are visible to it after the barrier;
+      // one wavefront normalises and quantises it as rmsnorm_quantize_rows
+      __shared__ float xt[kRmsRowLds<4>];
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        switch (H >> 8) {
+          case 1:
+            rms_quant_row<1>(o, nrm.w, nrm.eps, nrm.aq, nrm.asc, row, true, lane, xt);
+            break;
+          case 2:
+            rms_quant_row<2>(o, nrm.w, nrm.eps, nrm.aq, nrm.asc, row, true, lane, xt);
+            break;
+          case 3:
+            rms_quant_row<3>(o, nrm.w, nrm.eps, nrm.aq, nrm.asc, row, true, lane, xt);
+            break;
+          default:
+            rms_quant_row<4>(o, nrm.w, nrm.eps, nrm.aq, nrm.asc, row, true, lane, xt);
+            break;
+        }
+      }
     }
     return;
   }
@@ -661,6 +693,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // the residual GEMMs' fused norm: tile-major codes, the int8 form, the
   // 32-row residual tiles (below 2048 rows)
   const bool nfuse = L.norm_fused && tiled && !f16 && T < 2048;
+  const bool emb_norm = nfuse && C <= ovh::kEmbMaxC && !L.layers.empty();
   if (nfuse && ovh::band_counter_words(T) > L.band_words) {
     // before any capture; the old counters may still be in use by the stream
     OVH_HIP(hipStreamSynchronize(L.st), "hipStreamSynchronize");
@@ -882,8 +915,10 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         OVH_HIP(hipGetLastError(), "mask_to_bias launch");
       }
     }
+    // with nfuse, the first layer's input norm runs in the embedding launch
+    const ovh::EmbNorm en{emb_norm ? L.layers[0].ln1 : nullptr, c.rms_eps, aq, asc};
     hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)(T + mask_wgs)), dim3(256), 0, st, d_ids,
-                       d_am, seq, (int)C, H, L.tok, L.aud, L.d_offsets, x, T, mj);
+                       d_am, seq, (int)C, H, L.tok, L.aud, L.d_offsets, x, T, mj, en);
     OVH_HIP(hipGetLastError(), "embed launch");
     const int64_t qkv_n[3] = {QD, KVD, KVD};
     float* qkv_c[3] = {q, k, v};
@@ -891,8 +926,9 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     float* gu_c[2] = {gate, up};
     for (size_t li = 0; li < L.layers.size(); ++li) {
       const OvhLm::Layer& Y = L.layers[li];
-      // with nfuse, the previous layer's down launch normalised x into aq/asc
-      if ((li == 0 || !nfuse) && (rc = norm_q(Y.ln1)) != OV_OK) return rc;
+      // with nfuse, the embedding launch (layer 0) or the previous layer's down
+      // launch normalised x into aq/asc
+      if (!(li == 0 ? emb_norm : nfuse) && (rc = norm_q(Y.ln1)) != OV_OK) return rc;
       if (qkv_fused) {
         // q/k/v GEMM + qk-norm/RoPE + K/V planes in one launch, then attention
         ovh::GemmArgs ga;
