@@ -672,6 +672,36 @@ def test_linear_q_norm_equals_two_calls(oracle, M, N, K):
     assert host(cnt)[0] == 0  # no hand-off wait ran out
 
 
+def test_linear_q_norm_wait_running_out_is_flagged(oracle):
+    """A helper whose wait for the rest of its band runs out flags the counter
+    buffer's error word (the condition forced from the host: band 0's counter
+    set to 1, so the band's last arrival waits for a count the launch never
+    reaches; its wait is bounded, ~0.1 s), and a clean buffer works again."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(5)
+    A, Wf = _rand_problem(rng, 32, 1024, 1024)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    t = ov.tile_major(aq)
+    nw = dev(rng.uniform(0.5, 1.5, 1024).astype(np.float32))
+    cnt = ov.band_counters()
+    stride = 32  # 64-bit words per counter slot: the error word's slot, then band 0's
+    cnt[stride] = 1
+    ov.linear_q_norm(t, asc, w, dev(np.zeros((32, 1024), np.float32)), nw, cnt)
+    torch.cuda.synchronize()
+    assert host(cnt)[0] != 0
+    cnt.zero_()
+    x = dev(np.zeros((32, 1024), np.float32))
+    nq, nsc = ov.linear_q_norm(t, asc, w, x, nw, cnt)
+    want_x = dev(np.zeros((32, 1024), np.float32))
+    ov.linear_q_tiled(t, asc, w, 32, want_x, accumulate=True)
+    want_q, want_s = ov.rmsnorm_quantize(want_x, nw, 1e-6)
+    assert host(cnt)[0] == 0
+    assert np.array_equal(host(nq), tile_major(host(want_q), 32))
+    assert np.array_equal(bits(host(nsc)), bits(host(want_s)))
+
+
 def test_linear_q_norm_errors(oracle):
     import ovnative_amd as ov
     q, s = oracle.quantize_weight_rows(np.ones((1024, 1100), np.float32) * 0.01)
