@@ -334,7 +334,7 @@ def time_residual(cfg: dict, layers: int, M: int, reps: int = 4, eager: bool = T
         nw = [torch.rand(H, generator=g, device="cuda") + 0.5 for _ in range(2)]
         nq = torch.zeros(lib.ovh_tiled_codes_bytes(M, H), dtype=torch.int8, device="cuda")
         nsc = torch.empty((M, H // 32), device="cuda")
-        cnt = ov.band_counters()
+        cnt = ov.band_counters(M)
 
         def launches_norm(st):
             for a, b in zip(wo, wd):

@@ -134,19 +134,19 @@ int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhW
  * rmsnorm_quantize_f32 of the updated rows (lm.cpp:292 and :232,
  * gemm.cpp:638-707) with weight nw into codes nq (tile-major,
  * ovh_tiled_codes_bytes(M, N)) and scales nsc [M][N / 32]; x, nq and nsc hold
- * the bits of those two calls.  N = 256 P with P <= 4, K a multiple of 128,
- * M < 2048.  band_cnt: ovh_band_counter_bytes() of device memory, zeroed by
+ * the bits of those two calls.  N = 256 P with P <= 4, K a multiple of 128.
+ * band_cnt: ovh_band_counter_bytes(R) of device memory, R >= M, zeroed by
  * the caller before its first use, then passed unchanged to every later call
  * on that device with the same N (each launch advances its counters); calls
  * sharing one run in stream order.  Its first 4 bytes turn non-zero if a
- * workgroup's wait for the rest of its 32-row band ran out (only possible
+ * workgroup's wait for the rest of its row band ran out (only possible
  * when other work keeps the device from holding the band's workgroups); the
  * outputs of that call are then not to be used.  No reference counterpart as
  * one call (the LM runner's o_proj / down launch). */
 int ovh_linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
                       int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
                       void* band_cnt, void* stream);
-int64_t ovh_band_counter_bytes(void);
+int64_t ovh_band_counter_bytes(int64_t max_rows);
 /* linear_s8_nk_packed_q_sliced (ov_gemm.h:105-111, gemm.cpp:776-827): one launch
  * over a concatenated weight, slice s (N = slice_n[s], a positive multiple of
  * 64, summing to the weight's N) written to slice_c[s] with leading dimension

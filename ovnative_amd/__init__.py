@@ -48,7 +48,7 @@ SIGNATURES = {
     "ovh_linear_q_sliced": (_int, [_i64, _p, _p, _p, _p, _p, _int, _p]),
     "ovh_linear_q_tiled": (_int, [_i64, _p, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_q_norm": (_int, [_i64, _p, _p, _p, _p, _i64, _p, _f32, _p, _p, _p, _p]),
-    "ovh_band_counter_bytes": (_i64, []),
+    "ovh_band_counter_bytes": (_i64, [_i64]),
     "ovh_linear": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_linear_noalloc": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_weight_upload_f32": (_int, [_i64, _i64, _p, _int, _p, C.POINTER(_p)]),
@@ -337,11 +337,13 @@ def linear_q_tiled(aq_tiled, asc, w: Weight, M: int, C=None, accumulate: bool = 
     return C
 
 
-def band_counters():
-    """Zeroed device memory for linear_q_norm's band counters: allocate one per
-    device and output width N, and pass it to every call (stream-ordered)."""
+def band_counters(max_rows: int = 2048):
+    """Zeroed device memory for linear_q_norm's band counters, for calls of up
+    to max_rows rows: allocate one per device and output width N, and pass it
+    to every call (stream-ordered)."""
     torch = _torch()
-    return torch.zeros(load().ovh_band_counter_bytes() // 8, dtype=torch.int64, device="cuda")
+    return torch.zeros(load().ovh_band_counter_bytes(max_rows) // 8, dtype=torch.int64,
+                       device="cuda")
 
 
 def linear_q_norm(aq_tiled, asc, w: Weight, x, nw, band_cnt, eps: float = 1e-6):

@@ -544,10 +544,12 @@ int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhW
   return ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), true);
 }
 
-// band_cnt: the hand-off error word in the first counter slot, then one slot
-// per 32-row band (band_counter_words(2048): every M the entry point takes)
-int64_t ovh_band_counter_bytes(void) {
-  return (int64_t)sizeof(unsigned long long) * (ovh::kBandCntStride + ovh::band_counter_words(2048));
+// band_cnt: the hand-off error word in the first counter slot, then the band
+// slots for launches of up to max_rows rows (band_counter_words)
+int64_t ovh_band_counter_bytes(int64_t max_rows) {
+  if (max_rows < 1) max_rows = 1;
+  return (int64_t)sizeof(unsigned long long) *
+         (ovh::kBandCntStride + ovh::band_counter_words(max_rows));
 }
 
 int ovh_linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
@@ -555,7 +557,6 @@ int ovh_linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWe
                       void* band_cnt, void* stream) {
   if (M <= 0) return OV_OK;
   if (!w) return fail(OV_ERR_INVALID_ARG, "weight is null");
-  if (M >= 2048) return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_norm: M must be below 2048");
   if (w->w.Kb % 4 != 0)
     return fail(OV_ERR_NOT_IMPLEMENTED, "linear_q_norm: K must be a multiple of 128");
   if (w->w.N % 256 != 0 || w->w.N > 1024)

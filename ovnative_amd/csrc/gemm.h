@@ -30,8 +30,13 @@ enum GemmMode {
 // advance by the number of column tiles per launch.
 constexpr int kMaxNormHelpers = 32;
 constexpr int kBandCntStride = 32;
-// 64-bit words of band counters for M rows
-inline int64_t band_counter_words(int64_t M) { return (M + 31) / 32 * kBandCntStride; }
+// Counter slots: the 32-row bands of launches below 2048 rows take slots
+// 0 .. 63, the 64-row bands from 2048 rows slots kLargeMBandBase on.
+constexpr int kLargeMBandBase = 64;
+// 64-bit words of band counters for launches of up to M rows
+inline int64_t band_counter_words(int64_t M) {
+  return (kLargeMBandBase + (M + 63) / 64) * kBandCntStride;
+}
 
 // kQkvNorm: the runner's merged q/k/v GEMM with qk_norm_rope_f32 and the
 // split-f16 attention's K/V planes in its epilogue.  Each 128-column output

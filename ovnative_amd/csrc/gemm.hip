@@ -895,7 +895,7 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     // stores are in the XCD's L2, where the band's counter add is performed
     // after them (atomics execute in L2; the counter's 256-byte line is this
     // band's alone, so no other XCD holds it).
-    static_assert(BN == 32 && BM == 32, "bands of 32 rows, 32-column tiles");
+    static_assert(BM % 32 == 0, "bands of whole 32-row block tiles");
     static_assert(NW * kRmsRowLds<4> * 4 + 16 <= NST * STAGE, "the row norm's LDS fits in the ring");
     wait_vm_lgkm<0>();
     __syncthreads();  // every wavefront's stores drained; the ring is free
@@ -1053,8 +1053,8 @@ hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
   return launch_qkv_cfg<32, true, false>(a, st);
 }
 
-// The residual GEMM followed by the row norm of its result (kAccumNorm):
-// 32 x 32 tiles, all of a 32-row band on one XCD.
+// The residual GEMM followed by the row norm of its result (kAccumNorm): the
+// residual tiles with all of a BM-row band on one XCD.
 // Helpers per band: as many as the waiting ones leave the bands' other
 // workgroups room.  A band's waiting workgroups (helpers - 1 at most) hold
 // their slots until the band completes; over the bands one XCD holds at once
@@ -1076,34 +1076,43 @@ int norm_helpers(int occ, int64_t bands) {
   return h;
 }
 
-template <int WM, int SB, int NST>
-hipError_t launch_norm_cfg(const GemmArgs& a, hipStream_t st) {
+template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
+hipError_t launch_norm_cfg(const GemmArgs& a, int64_t slot0, hipStream_t st) {
   if (a.Kb % SB) return hipErrorInvalidValue;
-  const int64_t n_tiles = ((int64_t)a.N + 31) / 32, m_tiles = ((int64_t)a.M + 31) / 32;
-  const dim3 grid((unsigned)(8 * n_tiles * ((m_tiles + 7) / 8))), block(128 * WM);
-  auto kernel = gemm16_kernel<32, 32, 2, WM, SB, NST, kAccumNorm, true>;
+  const int64_t n_tiles = ((int64_t)a.N + BN - 1) / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
+  const dim3 grid((unsigned)(8 * n_tiles * ((m_tiles + 7) / 8))), block(64 * WN * WM);
+  auto kernel = gemm16_kernel<BN, BM, WN, WM, SB, NST, kAccumNorm, PIPE>;
   // resident workgroups per CU: a property of this kernel on the architecture
   static const int occ = [&] {
     int o = 0;
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 128 * WM, 0) == hipSuccess ? o
-                                                                                              : 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, kernel, 64 * WN * WM, 0) ==
+                   hipSuccess
+               ? o
+               : 0;
   }();
   GemmArgs b = a;
+  b.band_cnt = a.band_cnt + slot0 * kBandCntStride;
   b.n_helpers = norm_helpers(occ, m_tiles);
   hipLaunchKernelGGL(kernel, grid, block, 0, st, b);
   return hipGetLastError();
 }
 
-// The tiles the residual mode takes below 2048 rows (launch_gemm).
+// The tiles the residual mode takes (launch_gemm).  Counter slots: the
+// 32-row bands below 2048 rows use slots 0 .. 63, the 64-row bands from 2048
+// rows slots kLargeMBandBase on; each class has one column-tile count per N,
+// which is what a slot's counter advances by per launch.
 hipError_t launch_gemm_norm(const GemmArgs& a, hipStream_t st) {
   if (a.Kb % 4 || a.nslices != 1 || !a.out[0] || !a.nw || !a.nq || !a.nsc || !a.band_cnt ||
-      !a.norm_err || a.N % 256 || a.N < 256 || a.N > 1024 || a.M >= 2048 || a.W16 || a.aq16)
+      !a.norm_err || a.N % 256 || a.N < 256 || a.N > 1024 || a.W16 || a.aq16)
     return hipErrorInvalidValue;
   const int64_t M = a.M;
-  if (M < 512 && a.Kb % 8 == 0) return launch_norm_cfg<2, 8, 3>(a, st);
-  if (M < 256) return launch_norm_cfg<2, 4, 3>(a, st);
-  if (M < 1024) return a.Kb % 8 == 0 ? launch_norm_cfg<2, 8, 2>(a, st) : launch_norm_cfg<2, 4, 3>(a, st);
-  return launch_norm_cfg<1, 4, 2>(a, st);
+  if (M >= 2048) return launch_norm_cfg<128, 64, 4, 2, 4, 2, false>(a, kLargeMBandBase, st);
+  if (M < 512 && a.Kb % 8 == 0) return launch_norm_cfg<32, 32, 2, 2, 8, 3, true>(a, 0, st);
+  if (M < 256) return launch_norm_cfg<32, 32, 2, 2, 4, 3, true>(a, 0, st);
+  if (M < 1024)
+    return a.Kb % 8 == 0 ? launch_norm_cfg<32, 32, 2, 2, 8, 2, true>(a, 0, st)
+                         : launch_norm_cfg<32, 32, 2, 2, 4, 3, true>(a, 0, st);
+  return launch_norm_cfg<32, 32, 2, 1, 4, 2, true>(a, 0, st);
 }
 
 template <int BN, int BM, int WN, int WM, int SB>

@@ -690,8 +690,9 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
       f16 = ovh::weight_f16(Y.qkv, L.st) && ovh::weight_f16(Y.o, L.st) &&
             ovh::weight_f16(Y.gate_up, L.st) && ovh::weight_f16(Y.down, L.st);
   if (f16 && !L.head->f32) f16 = ovh::weight_f16(L.head, L.st);
-  // the residual GEMMs' fused norm: tile-major codes, the int8 form, the
-  // 32-row residual tiles (below 2048 rows)
+  // the residual GEMMs' fused norm: tile-major codes, the int8 GEMM form,
+  // below 2048 rows (from there, on 64-row bands, it measured no faster than
+  // the separate norm: config 5 forward 39.5 against 39.4 ms)
   const bool nfuse = L.norm_fused && tiled && !f16 && T < 2048;
   const bool emb_norm = nfuse && C <= ovh::kEmbMaxC && !L.layers.empty();
   if (nfuse && ovh::band_counter_words(T) > L.band_words) {

@@ -38,8 +38,8 @@ int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeig
 // x [M][ldx] += linear_q(aq, w) (N = w's N, tile-major codes), then
 // rmsnorm_quantize of the updated rows with weight nw into codes nq
 // (tile-major) and scales nsc, in the same launch (GemmMode kAccumNorm:
-// M < 2048, N = 256 P with P <= 4, K a multiple of 128).  band_cnt: the
-// launch's band counters (band_counter_words(M), zero when allocated, kept
+// N = 256 P with P <= 4, K a multiple of 128).  band_cnt: the launch's band
+// counters (band_counter_words(M) or more, zero when allocated, kept
 // for every later launch with the same N); err gets bit 2 if a hand-off wait
 // ran out.
 int linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,

@@ -638,14 +638,15 @@ def test_linear_q_tiled_equals_rowmajor(oracle, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(600, 1024, 2048), (600, 1024, 3072), (128, 1024, 3072),
                                    (1, 1024, 2048), (37, 256, 512), (300, 512, 1024),
-                                   (1320, 1024, 2048), (2047, 768, 1024)])
+                                   (1320, 1024, 2048), (2047, 768, 1024), (2048, 1024, 2048),
+                                   (4133, 1024, 3072), (2400, 256, 1024)])
 def test_linear_q_norm_equals_two_calls(oracle, M, N, K):
     """ovh_linear_q_norm (the runner's o_proj / down launch, with the RMSNorm +
     quantise that follows it: lm.cpp:281 + :292, :311 + :232) gives the bits of
     ovh_linear_q_tiled in its residual form followed by ovh_rmsnorm_quantize,
-    codes tile-major, over repeated calls on one counter buffer; the norm's
-    codes and scales are also the oracle's rmsnorm_quantize of the updated
-    rows."""
+    codes tile-major, over repeated calls on one counter buffer (32-row bands
+    below 2048 rows, 64-row bands from 2048); the norm's codes and scales are
+    also the oracle's rmsnorm_quantize of the updated rows."""
     import ovnative_amd as ov
     rng = np.random.default_rng(7 * M + N + K)
     A, Wf = _rand_problem(rng, M, N, K)
@@ -655,7 +656,7 @@ def test_linear_q_norm_equals_two_calls(oracle, M, N, K):
     t = ov.tile_major(aq)
     nw_h = rng.uniform(0.1, 1.1, N).astype(np.float32)
     nw = dev(nw_h)
-    cnt = ov.band_counters()
+    cnt = ov.band_counters(M)
     Cin = rng.standard_normal((M, N)).astype(np.float32)
     want_x = dev(Cin)
     ov.linear_q_tiled(t, asc, w, M, want_x, accumulate=True)
