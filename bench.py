@@ -524,10 +524,13 @@ def linear_inputs(M=256, K=1024, N=3072, seed=1234):
 
 
 def run_linear(args) -> None:
-    """s8_nk_quantize of A then linear_s8_nk_packed_q, through
-    the C ABI (ovh_s8_nk_quantize + ovh_linear_q) on device-resident inputs.  One
-    step = the pair of launches; the GEMM alone is timed too for its roofline
-    (HBM-bound: 6.60 MB of algorithmic traffic against 1.61 GOP)."""
+    """the int8-nk linear of fp32 activations,
+    linear_s8_nk_packed (quantise A per 32-k block, then the int8 GEMM) as
+    ovh_linear on device-resident inputs: one step = that call (its codes
+    tile-major inside).  Also timed: the reference's q path as two calls
+    (ovh_s8_nk_quantize + ovh_linear_q, row-major codes), and the GEMM alone on
+    tile-major codes for the roofline (HBM-bound: 6.60 MB of algorithmic
+    traffic against 1.61 GOP)."""
     import numpy as np
     import torch
     import ovnative_amd as ov
@@ -543,6 +546,9 @@ def run_linear(args) -> None:
     C_ = torch.empty((M, N), dtype=torch.float32, device="cuda")
     qargs = (M, K, dA.data_ptr(), aq.data_ptr(), asc.data_ptr(), st)
     largs = (M, aq.data_ptr(), asc.data_ptr(), w.handle, C_.data_ptr(), N, 0, st)
+    fargs = (M, dA.data_ptr(), w.handle, C_.data_ptr(), N, 0, st)
+    aqt = ov.tile_major(ov.s8_nk_quantize(dA)[0])
+    targs = (M, aqt.data_ptr(), asc.data_ptr(), w.handle, C_.data_ptr(), N, 0, st)
 
     def timed(fns, reps):
         for _ in range(args.warmup):
@@ -561,14 +567,17 @@ def run_linear(args) -> None:
 
     t0 = time.perf_counter()
     reps = max(args.steps, 200)
+    ms_step = timed([(lib.ovh_linear, fargs)], reps)
     ms_pair = timed([(lib.ovh_s8_nk_quantize, qargs), (lib.ovh_linear_q, largs)], reps)
-    ms_gemm = timed([(lib.ovh_linear_q, largs)], reps)
+    ms_gemm_rm = timed([(lib.ovh_linear_q, largs)], reps)
+    ms_gemm = timed([(lib.ovh_linear_q_tiled, targs)], reps)
     ms_quant = timed([(lib.ovh_s8_nk_quantize, qargs)], reps)
     wall = time.perf_counter() - t0
     ops = 2 * M * N * K
     gemm_bytes = N * K + 4 * N + M * 32 * Kb + 4 * M * Kb + 4 * M * N
-    log(f"config 1: quantise + linear {ms_pair * 1e3:.2f} us (quantise {ms_quant * 1e3:.2f}, "
-        f"linear {ms_gemm * 1e3:.2f}); linear {gemm_bytes / ms_gemm / 1e6:.0f} GB/s")
+    log(f"config 1: ovh_linear {ms_step * 1e3:.2f} us; as two calls {ms_pair * 1e3:.2f} us "
+        f"(quantise {ms_quant * 1e3:.2f}, linear {ms_gemm_rm * 1e3:.2f}); the GEMM on tile-major "
+        f"codes {ms_gemm * 1e3:.2f} us = {gemm_bytes / ms_gemm / 1e6:.0f} GB/s")
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -603,14 +612,16 @@ def run_linear(args) -> None:
                    "ms_per_step": round(sec * 1e3, 4)}
     frac_gb = gemm_bytes / ms_gemm / 1e6
     line = bench_line(
-        args, round(ops / (ms_pair * 1e-3) / 1e12, 2), "TOPS", round(ms_pair, 5),
-        {"workload": (f"BASELINE config 1: s8_nk_quantize of A fp32 [{M},{K}] (~N(0,1), 8 outlier "
-                      f"channels x20) + int8-nk linear to C fp32 [{M},{N}] (W ~N(0,0.02), per-channel "
-                      "int8), inputs resident in HBM"),
+        args, round(ops / (ms_step * 1e-3) / 1e12, 2), "TOPS", round(ms_step, 5),
+        {"workload": (f"BASELINE config 1: ovh_linear (linear_s8_nk_packed): A fp32 [{M},{K}] "
+                      f"(~N(0,1), 8 outlier channels x20) quantised per 32-k block, then the "
+                      f"int8-nk linear to C fp32 [{M},{N}] (W ~N(0,0.02), per-channel int8), inputs "
+                      "resident in HBM"),
          "model": "single linear (MLP up-proj shape)", "global_batch": M, "seq_len": 1,
-         "parallelism": "single GPU", "quantize_ms": round(ms_quant, 5),
-         "linear_ms": round(ms_gemm, 5)},
-        {"bound": "hbm", "kernel": f"gemm16 store (M={M}, N={N}, K={K})",
+         "parallelism": "single GPU", "two_calls_ms": round(ms_pair, 5),
+         "quantize_ms": round(ms_quant, 5), "linear_rowmajor_ms": round(ms_gemm_rm, 5),
+         "linear_tiled_ms": round(ms_gemm, 5)},
+        {"bound": "hbm", "kernel": f"gemm16 store, tile-major codes (M={M}, N={N}, K={K})",
          "achieved": round(frac_gb, 1), "peak": 8000.0, "unit": "GB/s",
          "frac": round(frac_gb / 8000.0, 4),
          "traffic": residual_traffic("gemm_linear_m256_traffic.json"), "avg_ms": round(ms_gemm, 5),

@@ -604,26 +604,100 @@ int ovh_linear_q_grouped(const OvhGemmGroup* groups, int n_groups, int accumulat
   return OV_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// ovh_linear's quantised copy of A.  One workspace per (device, stream), kept
+// from the first call on that stream until the process ends and grown when a
+// call needs more: calls on one stream are ordered by the stream, calls on
+// different streams never share one.  Growth frees the old buffer and
+// allocates the new one on the calling stream (hipFreeAsync/hipMallocAsync),
+// after that stream's earlier work.  Under graph capture a call that does not
+// fit the workspace allocates and frees in the graph instead, leaving the
+// workspace as it is.  A stream destroyed while a call on it is still running
+// must not be replaced by a new stream of the same handle before that call
+// ends.
+struct LinearWorkspace {
+  int device;
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+constexpr int kMaxLinearWorkspaces = 256;
+std::mutex g_ws_mu;
+LinearWorkspace g_ws[kMaxLinearWorkspaces];
+int g_ws_n = 0;
+
+// The workspace of the current device and stream st with at least `bytes`
+// (*ptr), or *ptr = nullptr and *owned = true after a stream-ordered
+// allocation the caller frees (capture, or more streams than the table holds).
+int linear_workspace(hipStream_t st, size_t bytes, void** ptr, bool* owned) {
+  *ptr = nullptr;
+  *owned = false;
+  int dev = 0;
+  OVH_HIP(hipGetDevice(&dev), "hipGetDevice");
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  OVH_HIP(hipStreamIsCapturing(st, &cap), "hipStreamIsCapturing");
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  LinearWorkspace* ws = nullptr;
+  for (int i = 0; i < g_ws_n; ++i)
+    if (g_ws[i].device == dev && g_ws[i].stream == st) ws = &g_ws[i];
+  if (ws && ws->bytes >= bytes) {
+    *ptr = ws->ptr;
+    return OV_OK;
+  }
+  if (cap != hipStreamCaptureStatusNone || (!ws && g_ws_n == kMaxLinearWorkspaces)) {
+    OVH_HIP(hipMallocAsync(ptr, bytes, st), "hipMallocAsync(linear workspace)");
+    *owned = true;
+    return OV_OK;
+  }
+  if (!ws) {
+    ws = &g_ws[g_ws_n++];
+    *ws = LinearWorkspace{dev, st, nullptr, 0};
+  }
+  if (ws->ptr) {
+    (void)hipFreeAsync(ws->ptr, st);
+    ws->ptr = nullptr;
+    ws->bytes = 0;
+  }
+  const size_t grown = bytes + bytes / 4;  // room for a somewhat larger M next time
+  OVH_HIP(hipMallocAsync(&ws->ptr, grown, st), "hipMallocAsync(linear workspace)");
+  ws->bytes = grown;
+  *ptr = ws->ptr;
+  return OV_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t ldc,
                int accumulate, void* stream) {
   if (M <= 0) return OV_OK;
   if (!w || !A) return fail(OV_ERR_INVALID_ARG, "null argument");
   const hipStream_t st = as_stream(stream);
-  int8_t* aq = nullptr;
-  float* asc = nullptr;
-  OVH_HIP(hipMallocAsync(reinterpret_cast<void**>(&aq), (size_t)(M * w->w.Kp), st),
-          "hipMallocAsync(aq)");
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&asc),
-                                sizeof(float) * (size_t)(M * w->w.Kb), st);
-  int rc = OV_OK;
-  if (e != hipSuccess) {
-    rc = hip_fail(e, "hipMallocAsync(asc)");
+  // K a multiple of 128: the codes tile-major (the layout the 16x16 GEMM reads
+  // as contiguous 1 KiB tiles), else row-major; the scales [M][Kb] follow at
+  // the next 256-byte boundary
+  const bool tiled = w->w.Kb % 4 == 0;
+  const size_t code_bytes =
+      ((tiled ? (size_t)ovh_tiled_codes_bytes(M, w->w.K) : (size_t)M * (size_t)w->w.Kp) + 255) &
+      ~(size_t)255;
+  void* ws = nullptr;
+  bool owned = false;
+  int rc = linear_workspace(st, code_bytes + sizeof(float) * (size_t)M * (size_t)w->w.Kb, &ws,
+                            &owned);
+  if (rc != OV_OK) return rc;
+  int8_t* aq = static_cast<int8_t*>(ws);
+  float* asc = reinterpret_cast<float*>(aq + code_bytes);
+  if (tiled) {
+    const hipError_t e = ovh::launch_quantize(M, w->w.K, A, aq, asc, st, true);
+    rc = e == hipSuccess ? ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, st, true)
+                         : hip_fail(e, "quantize launch");
   } else {
     rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
     if (rc == OV_OK) rc = ovh_linear_q(M, aq, asc, w, C, ldc, accumulate, stream);
   }
-  (void)hipFreeAsync(aq, st);
-  if (asc) (void)hipFreeAsync(asc, st);
+  if (owned) (void)hipFreeAsync(ws, st);
   return rc;
 }
 
@@ -689,11 +763,17 @@ int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, 
                        int accumulate, void* stream) {
   if (M <= 0) return OV_OK;
   if (!w || !A) return fail(OV_ERR_INVALID_ARG, "null argument");
-  // codes [M][Kp] at offset 0, scales [M][Kb] at the next 256-byte boundary;
-  // the quantiser writes every byte of both (K-tail padding included), so
-  // nothing has to start at zero
-  const size_t code_bytes = ((size_t)M * (size_t)w->w.Kp + 255) & ~(size_t)255;
-  const size_t need = code_bytes + sizeof(float) * (size_t)M * (size_t)w->w.Kb;
+  // codes at offset 0 ([M][Kp], or tile-major as in ovh_linear when K is a
+  // multiple of 128 and the rows padded to 128 still fit), scales [M][Kb] at
+  // the next 256-byte boundary; the quantiser writes every code and scale the
+  // GEMM uses (K-tail padding included; rows of a tile past M are read but
+  // their outputs dropped), so nothing has to start at zero
+  const size_t scale_bytes = sizeof(float) * (size_t)M * (size_t)w->w.Kb;
+  const size_t tiled_bytes = ((size_t)ovh_tiled_codes_bytes(M, w->w.K) + 255) & ~(size_t)255;
+  const bool tiled = w->w.Kb % 4 == 0 && tiled_bytes + scale_bytes <= kNoAllocScratchBytes;
+  const size_t code_bytes =
+      tiled ? tiled_bytes : ((size_t)M * (size_t)w->w.Kp + 255) & ~(size_t)255;
+  const size_t need = code_bytes + scale_bytes;
   if (M > ((int64_t)1 << 31) || need > kNoAllocScratchBytes)
     return fail(OV_ERR_INVALID_ARG,
                 "linear_noalloc: M * (Kp + 4 * Kb) = " + std::to_string(need) +
@@ -703,10 +783,15 @@ int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, 
   if (rc != OV_OK) return rc;
   int8_t* aq = static_cast<int8_t*>(base);
   float* asc = reinterpret_cast<float*>(static_cast<char*>(base) + code_bytes);
-  rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
+  if (tiled) {
+    const hipError_t e = ovh::launch_quantize(M, w->w.K, A, aq, asc, as_stream(stream), true);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  } else {
+    rc = ovh_s8_nk_quantize(M, w->w.K, A, aq, asc, stream);
+  }
   // the int8 GEMM form at every M (the f16 form would allocate)
   if (rc == OV_OK)
-    rc = ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), false, nullptr, false);
+    rc = ovh::linear_q(M, aq, asc, w, C, ldc, accumulate, as_stream(stream), tiled, nullptr, false);
   return rc;
 }
 

@@ -12,6 +12,7 @@ namespace ovh {
 
 // ---------------------------------------------------------------------------
 // s8_nk_quantize: cpp/src/backend/cpu/gemm.cpp:379-430 (quantize_a_u8).
+// Codes row-major [M][Kp].
 template <bool VEC4>
 __global__ __launch_bounds__(256) void quantize_kernel(int64_t M, int64_t K, int64_t Kb,
                                                        const float* __restrict__ A,
@@ -39,6 +40,61 @@ __global__ __launch_bounds__(256) void quantize_kernel(int64_t M, int64_t K, int
   *reinterpret_cast<uint32_t*>(aq + m * Kb * 32 + b * 32 + sub * 4) = codes;
   if (sub == 0) asc[m * Kb + b] = s;
 }
+
+// The same quantiser into tile-major codes.  Codes of one 32-row x 32-k tile
+// are 8-byte row pieces spread over 1 KiB, so lanes that each own a row's 4
+// codes write scattered 4-byte pieces; when the 16 rows of a code line come
+// from different workgroups on different XCDs, each XCD's L2 writes back its
+// own partial copy of the line.  Here one workgroup owns TB whole tiles (a
+// 32-row band x TB blocks, TB KiB contiguous in act_index order), builds them
+// in LDS and stores them as 16-byte vectors; rows of the band past M get zero
+// codes.  Each 8-lane group quantises one (row, block) as quantize_kernel
+// does, so codes and scales are the same bits.
+template <bool VEC4, int TB>
+__global__ __launch_bounds__(256) void quantize_tiles_kernel(int64_t M, int64_t K, int64_t Kb,
+                                                             const float* __restrict__ A,
+                                                             int8_t* __restrict__ aq,
+                                                             float* __restrict__ asc) {
+  __shared__ __attribute__((aligned(16))) int8_t tiles[TB * 1024];
+  const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
+  const int64_t m0 = (int64_t)blockIdx.x * 32, b0 = (int64_t)blockIdx.y * TB;
+  // pass p: (row, block) group p*32 + grp = rr*TB + j; every load first
+  float v[TB][4];
+  int nvalid[TB];
+#pragma unroll
+  for (int p = 0; p < TB; ++p) {
+    const int gi = p * 32 + grp, j = gi % TB, rr = gi / TB;
+    const int64_t m = m0 + rr, b = b0 + j, k0 = b * 32 + sub * 4, rem = K - k0;
+    nvalid[p] = m < M && b < Kb ? (rem >= 4 ? 4 : (rem > 0 ? (int)rem : 0)) : 0;
+    const float* row = A + (m < M ? m : 0) * K;
+    if (VEC4 && nvalid[p] == 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(row + k0);
+      v[p][0] = x[0]; v[p][1] = x[1]; v[p][2] = x[2]; v[p][3] = x[3];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[p][e] = e < nvalid[p] ? row[k0 + e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < TB; ++p) {
+    const int gi = p * 32 + grp, j = gi % TB, rr = gi / TB;
+    const int64_t m = m0 + rr, b = b0 + j;
+    uint32_t codes;
+    const float sc = quant_block_lane(v[p], nvalid[p], &codes);
+    *reinterpret_cast<uint32_t*>(tiles + j * 1024 + act_index(rr, sub * 4, 32, true)) = codes;
+    if (sub == 0 && m < M && b < Kb) asc[m * Kb + b] = sc;
+  }
+  __syncthreads();
+  const int64_t nb = Kb - b0 < TB ? Kb - b0 : TB;
+  int8_t* const dst = aq + act_index(m0, b0 * 32, Kb * 32, true);
+#pragma unroll
+  for (int p = 0; p < (TB + 3) / 4; ++p) {
+    const int64_t o = (int64_t)(p * 256 + threadIdx.x) * 16;
+    if (o < nb * 1024)
+      *reinterpret_cast<int4*>(dst + o) = *reinterpret_cast<const int4*>(tiles + o);
+  }
+}
+constexpr int kQuantTilesPerWg = 1;  // 1, 2, 4 measured: 1 fastest at M = 256, K = 1024
 
 // ---------------------------------------------------------------------------
 // rmsnorm_quantize_f32: cpp/src/backend/cpu/gemm.cpp:638-707.
@@ -230,8 +286,19 @@ __global__ __launch_bounds__(256) void silu_mul_quantize_kernel(
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 hipError_t launch_quantize(int64_t M, int64_t K, const float* A, int8_t* aq, float* asc,
-                           hipStream_t st) {
+                           hipStream_t st, bool tiled) {
   const int64_t Kb = kb_of(K);
+  if (tiled) {
+    constexpr int TB = kQuantTilesPerWg;
+    const dim3 grid((unsigned)((M + 31) / 32), (unsigned)((Kb + TB - 1) / TB)), block(256);
+    if (K % 4 == 0 && aligned16(A))
+      hipLaunchKernelGGL((quantize_tiles_kernel<true, TB>), grid, block, 0, st, M, K, Kb, A, aq,
+                         asc);
+    else
+      hipLaunchKernelGGL((quantize_tiles_kernel<false, TB>), grid, block, 0, st, M, K, Kb, A, aq,
+                         asc);
+    return hipGetLastError();
+  }
   const int64_t groups = M * Kb;
   const dim3 grid((unsigned)((groups + 31) / 32)), block(256);
   if (K % 4 == 0 && aligned16(A))

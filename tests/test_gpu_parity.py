@@ -467,6 +467,62 @@ def test_linear_quantizes_internally(oracle):
     assert np.array_equal(bits(host(Cacc)), bits(_oracle_linear(oracle, A, q, s, Cin)))
 
 
+# tile-major codes inside (K = 1000: a K tail; 994: no 4-float vector loads),
+# then row-major codes (K = 96)
+@pytest.mark.parametrize("K", [1024, 1000, 994, 96])
+def test_linear_workspace_growth_and_streams(oracle, K):
+    """ovh_linear keeps its quantised copy of A per stream and grows it: rows
+    rising and falling on the current stream and on a second stream, every
+    result against the oracle."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(K)
+    _, Wf = _rand_problem(rng, 1, 256, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    side = torch.cuda.Stream()
+    for M in (40, 700, 17, 1500, 300):
+        A, _ = _rand_problem(rng, M, 1, K)
+        want = bits(_oracle_linear(oracle, A, q, s))
+        assert np.array_equal(bits(host(ov.linear(dev(A), w))), want), M
+        dA = dev(A)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            C = ov.linear(dA, w)
+        torch.cuda.current_stream().wait_stream(side)
+        assert np.array_equal(bits(host(C)), want), M
+
+
+def test_linear_in_a_graph(oracle):
+    """ovh_linear captured once its stream's workspace fits: every replay
+    equals the eager result, with eager calls on that stream in between."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(21)
+    A, Wf = _rand_problem(rng, 200, 512, 1024)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    want = bits(_oracle_linear(oracle, A, q, s))
+    s0 = torch.cuda.Stream()
+    dA, C = dev(A), torch.zeros((200, 512), dtype=torch.float32, device="cuda")
+    A2, _ = _rand_problem(rng, 300, 1, 1024)
+    dA2 = dev(A2)
+    with torch.cuda.stream(s0):
+        ov.linear(dA2, w)                       # the workspace now holds 300 rows
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s0):
+        ov.linear(dA, w, C)
+    want2 = bits(_oracle_linear(oracle, A2, q, s))
+    for _ in range(3):
+        C.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(host(C)), want)
+        with torch.cuda.stream(s0):
+            C2 = ov.linear(dA2, w)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(host(C2)), want2)
+
+
 def test_ldc_and_slices_errors(oracle):
     import ovnative_amd as ov
     rng = np.random.default_rng(4)
