@@ -591,6 +591,26 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
         }
   };
 
+  // kQkvNorm: the epilogue's lookups (the QkvFuse block: segment table, plane
+  // pointers; the tile's column scales) come into LDS by DMA ahead of the
+  // ring's first stage, as older ops of wavefront 0, so the stage waits' counts
+  // are unchanged and the first stage barrier publishes them.
+  constexpr bool QKV = MODE == kQkvNorm;
+  constexpr int QF_OPS = (int)(sizeof(QkvFuse) / 16);
+  static_assert(sizeof(QkvFuse) % 16 == 0 && QF_OPS <= 64, "QkvFuse moves in 16-byte lanes");
+  __shared__ __attribute__((aligned(16))) float qkv_ws[QKV ? BN : 1];
+  __shared__ __attribute__((aligned(16))) int8_t qkv_f[QKV ? sizeof(QkvFuse) : 1];
+  if constexpr (QKV) {
+    if (wave == 0) {
+      if (lane < BN / 4)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.ws + n0 + 4 * lane),
+                                         (lds_void_t*)qkv_ws, 16, 0, 0);
+      if (lane < QF_OPS)
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(reinterpret_cast<const int8_t*>(a.qf) + 16 * lane),
+            (lds_void_t*)qkv_f, 16, 0, 0);
+    }
+  }
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s)
     if (s < nstages) issue(s);
@@ -659,12 +679,12 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     static_assert(BN == 128 && WN == 4 && FN == 2 && FM == 2 && 64 * NW == 8 * BM,
                   "kQkvNorm: 128-column tiles, 32 x 32 per wavefront, 8 threads per row");
     constexpr int NT = 64 * NW;
-    const QkvFuse& F = *a.qf;
+    const QkvFuse& F = *reinterpret_cast<const QkvFuse*>(qkv_f);
     const int QD = F.QD, KVD = F.KVD;
     float v[FN][FM][4];
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
-      const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + n0 + wn * 32 + i * 16 + 4 * q);
+      const f32x4 ws = *reinterpret_cast<const f32x4*>(&qkv_ws[wn * 32 + i * 16 + 4 * q]);
 #pragma unroll
       for (int j = 0; j < FM; ++j)
 #pragma unroll
