@@ -392,7 +392,17 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   constexpr int RH = BM > 64 ? 2 : 1;           // 64-row halves of the scale rows
   constexpr int SPH = SB >= 4 ? SB / 4 : SB;    // scale DMA ops per half and stage
   constexpr int SOPS = DUMP ? 0 : RH * SPH;     // scale DMA ops of the last wavefront per stage
-  __shared__ __attribute__((aligned(16))) int8_t smem[NST][STAGE];
+  // The q/k/v epilogue's column scales and QkvFuse block, fetched ahead of the
+  // K loop (below), sit after the ring in the one LDS array: with LDS objects
+  // of their own the compiler's wait insertion no longer sees that the stage
+  // loop's reads stay clear of the next stage's DMA, and waits for that DMA
+  // inside the loop.
+  constexpr bool QKV = MODE == kQkvNorm;
+  constexpr int QKV_WS = NST * STAGE, QKV_F = QKV_WS + (QKV ? BN * 4 : 0);
+  constexpr int LDS_BYTES = QKV_F + (QKV ? (int)sizeof(QkvFuse) : 0);
+  static_assert(QKV_WS % 16 == 0 && QKV_F % 16 == 0, "16-byte DMA slots");
+  __shared__ __attribute__((aligned(16))) int8_t lds[LDS_BYTES];
+  int8_t(&smem)[NST][STAGE] = *reinterpret_cast<int8_t(*)[NST][STAGE]>(lds);
 
   // wave index in a scalar register: the DMA slots and the wait below branch on it
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -595,11 +605,10 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   // pointers; the tile's column scales) come into LDS by DMA ahead of the
   // ring's first stage, as older ops of wavefront 0, so the stage waits' counts
   // are unchanged and the first stage barrier publishes them.
-  constexpr bool QKV = MODE == kQkvNorm;
   constexpr int QF_OPS = (int)(sizeof(QkvFuse) / 16);
   static_assert(sizeof(QkvFuse) % 16 == 0 && QF_OPS <= 64, "QkvFuse moves in 16-byte lanes");
-  __shared__ __attribute__((aligned(16))) float qkv_ws[QKV ? BN : 1];
-  __shared__ __attribute__((aligned(16))) int8_t qkv_f[QKV ? sizeof(QkvFuse) : 1];
+  float* const qkv_ws = reinterpret_cast<float*>(lds + QKV_WS);
+  const int8_t* const qkv_f = lds + QKV_F;
   if constexpr (QKV) {
     if (wave == 0) {
       if (lane < BN / 4)
