@@ -392,14 +392,16 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   constexpr int RH = BM > 64 ? 2 : 1;           // 64-row halves of the scale rows
   constexpr int SPH = SB >= 4 ? SB / 4 : SB;    // scale DMA ops per half and stage
   constexpr int SOPS = DUMP ? 0 : RH * SPH;     // scale DMA ops of the last wavefront per stage
-  // The q/k/v epilogue's column scales and QkvFuse block, fetched ahead of the
-  // K loop (below), sit after the ring in the one LDS array: with LDS objects
-  // of their own the compiler's wait insertion no longer sees that the stage
-  // loop's reads stay clear of the next stage's DMA, and waits for that DMA
-  // inside the loop.
+  // The epilogue's column scales (and the q/k/v epilogue's QkvFuse block),
+  // fetched ahead of the K loop (below), sit after the ring in the one LDS
+  // array: with LDS objects of their own the compiler's wait insertion no
+  // longer sees that the stage loop's reads stay clear of the next stage's
+  // DMA, and waits for that DMA inside the loop.
   constexpr bool QKV = MODE == kQkvNorm;
-  constexpr int QKV_WS = NST * STAGE, QKV_F = QKV_WS + (QKV ? BN * 4 : 0);
+  constexpr bool WSP = !DUMP && BN <= 256;  // column scales by DMA (one op)
+  constexpr int QKV_WS = NST * STAGE, QKV_F = QKV_WS + (WSP ? BN * 4 : 0);
   constexpr int LDS_BYTES = QKV_F + (QKV ? (int)sizeof(QkvFuse) : 0);
+  static_assert(!QKV || WSP, "the q/k/v epilogue reads its column scales from LDS");
   static_assert(QKV_WS % 16 == 0 && QKV_F % 16 == 0, "16-byte DMA slots");
   __shared__ __attribute__((aligned(16))) int8_t lds[LDS_BYTES];
   int8_t(&smem)[NST][STAGE] = *reinterpret_cast<int8_t(*)[NST][STAGE]>(lds);
@@ -607,13 +609,17 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   // are unchanged and the first stage barrier publishes them.
   constexpr int QF_OPS = (int)(sizeof(QkvFuse) / 16);
   static_assert(sizeof(QkvFuse) % 16 == 0 && QF_OPS <= 64, "QkvFuse moves in 16-byte lanes");
-  float* const qkv_ws = reinterpret_cast<float*>(lds + QKV_WS);
+  float* const qkv_ws = reinterpret_cast<float*>(lds + QKV_WS);  // column scales n0 ..
   const int8_t* const qkv_f = lds + QKV_F;
+  if constexpr (WSP) {
+    // chunks from n0 + 4 lane below N (the scale array is padded to a multiple
+    // of 128 columns, a tile may reach past it); the epilogue reads columns < N
+    if (wave == 0 && lane < BN / 4 && n0 + 4 * lane < a.N)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.ws + n0 + 4 * lane),
+                                       (lds_void_t*)qkv_ws, 16, 0, 0);
+  }
   if constexpr (QKV) {
     if (wave == 0) {
-      if (lane < BN / 4)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.ws + n0 + 4 * lane),
-                                         (lds_void_t*)qkv_ws, 16, 0, 0);
       if (lane < QF_OPS)
         __builtin_amdgcn_global_load_lds(
             static_cast<const void*>(reinterpret_cast<const int8_t*>(a.qf) + 16 * lane),
@@ -840,10 +846,10 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
       for (int pb = 0; pb < FN / 4; ++pb) {
         const int t = 4 * pb;
         const int nr = n0 + (wn * FN + t) * 16 + 4 * q;  // merged row of gate value e = 0
-        const f32x4 wg0 = *reinterpret_cast<const f32x4*>(a.ws + nr);
-        const f32x4 wu0 = *reinterpret_cast<const f32x4*>(a.ws + nr + 16);
-        const f32x4 wg1 = *reinterpret_cast<const f32x4*>(a.ws + nr + 32);
-        const f32x4 wu1 = *reinterpret_cast<const f32x4*>(a.ws + nr + 48);
+        const f32x4 wg0 = *reinterpret_cast<const f32x4*>(&qkv_ws[nr - n0]);
+        const f32x4 wu0 = *reinterpret_cast<const f32x4*>(&qkv_ws[nr - n0 + 16]);
+        const f32x4 wg1 = *reinterpret_cast<const f32x4*>(&qkv_ws[nr - n0 + 32]);
+        const f32x4 wu1 = *reinterpret_cast<const f32x4*>(&qkv_ws[nr - n0 + 48]);
         float h[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -889,7 +895,8 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     const int s0 = a.start[s], s1 = a.start[s + 1];
     const int nb = n16 + 4 * q;
     if (nb >= a.N) continue;
-    const f32x4 ws = *reinterpret_cast<const f32x4*>(a.ws + nb);
+    const f32x4 ws = WSP ? *reinterpret_cast<const f32x4*>(&qkv_ws[nb - n0])
+                         : *reinterpret_cast<const f32x4*>(a.ws + nb);
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int m = m0 + (wm * FM + j) * 16 + (lane & 15);
