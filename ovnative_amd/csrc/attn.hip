@@ -506,6 +506,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
 // runs in base 2 (scores scaled by log2(e), V_EXP_F32), and each wavefront loads
 // the K and V fragments of its next block while it computes the current one.
 constexpr int kQPad = kAttnD + 8;  // LDS row of a Q plane, in halves
+constexpr int kPartRow = kAttnD + 4;  // LDS row of a merge partial, in floats
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kMaskedLog2 = -1e29f * kLog2e;
 
@@ -516,8 +517,10 @@ template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, AttnSplit sp,
                                                                  int qtiles, int per_xcd) {
   // The Q planes (2 x 32 x kQPad halves) alias the start of `part`, which is
-  // written only after every wavefront has left the key loop.
-  __shared__ __attribute__((aligned(16))) float part[kAttnWaves][kAttnQ][kAttnD];
+  // written only after every wavefront has left the key loop.  Rows of `part`
+  // are padded by 16 bytes, so that the merge's reads (one query row per lane)
+  // spread over the banks.
+  __shared__ __attribute__((aligned(16))) float part[kAttnWaves][kAttnQ][kPartRow];
   __shared__ float mstat[kAttnWaves][kAttnQ], lstat[kAttnWaves][kAttnQ];
   __shared__ float alpha_s[kAttnWaves][kAttnQ];
   _Float16* qs_h = reinterpret_cast<_Float16*>(&part[0][0][0]);
@@ -542,28 +545,16 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int r32 = lane & 31, hf = lane >> 5;
 
-  // ---- Q rows q0..q0+31 of head h -> hi/lo planes in LDS (16 values per thread)
+  // ---- Q rows q0..q0+31 of head h (16 values per thread): loaded first, so
+  // that the K/V prefetch below is in flight while they are split into the
+  // hi/lo planes in LDS
+  const int q_row = threadIdx.x >> 3, q_c0 = (threadIdx.x & 7) * 16;
+  f32x4 qx[4];
   {
-    const int row = threadIdx.x >> 3, c0 = (threadIdx.x & 7) * 16;
-    const int qr = min(q0 + row, S - 1);
-    const float* src = args.q + seg.q_off + (int64_t)qr * args.q_stride + (int64_t)h * kAttnD + c0;
-    h8 hh[2], ll[2];
+    const int qr = min(q0 + q_row, S - 1);
+    const float* src = args.q + seg.q_off + (int64_t)qr * args.q_stride + (int64_t)h * kAttnD + q_c0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(src + 4 * j);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        _Float16 a, b;
-        split16(x[e], a, b);
-        hh[j >> 1][4 * (j & 1) + e] = a;
-        ll[j >> 1][4 * (j & 1) + e] = b;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      *reinterpret_cast<h8*>(qs_h + row * kQPad + c0 + 8 * j) = hh[j];
-      *reinterpret_cast<h8*>(qs_l + row * kQPad + c0 + 8 * j) = ll[j];
-    }
+    for (int j = 0; j < 4; ++j) qx[j] = *reinterpret_cast<const f32x4*>(src + 4 * j);
   }
 
   // Wave-uniform bases of this (KV head, segment)'s tiles and 32-bit per-lane
@@ -627,11 +618,33 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   constexpr bool kPrefetch = kBits;
   const int nblk = (S + kAttnK - 1) / kAttnK;
   const int nb = wave < nblk ? (nblk - 1 - wave) / kAttnWaves + 1 : 0;  // this wavefront's blocks
-  if (kPrefetch && nb > 0) {
-    load_k(wave * kAttnK);
-    load_v(wave * kAttnK);
+  if (kPrefetch) {  // unconditional (a wavefront without blocks loads one it will not use)
+    load_k(min(wave, nblk - 1) * kAttnK);
+    load_v(min(wave, nblk - 1) * kAttnK);
   }
-  __syncthreads();  // Q planes written
+  {
+    h8 hh[2], ll[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        _Float16 a, b;
+        split16(qx[j][e], a, b);
+        hh[j >> 1][4 * (j & 1) + e] = a;
+        ll[j >> 1][4 * (j & 1) + e] = b;
+      }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      *reinterpret_cast<h8*>(qs_h + q_row * kQPad + q_c0 + 8 * j) = hh[j];
+      *reinterpret_cast<h8*>(qs_l + q_row * kQPad + q_c0 + 8 * j) = ll[j];
+    }
+  }
+  // Q planes written: this wavefront's LDS stores done, then the barrier.  Not
+  // __syncthreads(), whose release fence would also wait for the K/V prefetch
+  // (vmcnt(0)); the empty asm keeps the compiler from moving LDS accesses
+  // across the barrier.
+  wait_vm_lgkm<63>();
+  asm volatile("s_barrier" ::: "memory");
 
   auto key_block = [&](int blk, auto next) __attribute__((always_inline)) {
     constexpr bool kNext = kPrefetch && decltype(next)::value;
@@ -770,8 +783,10 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     lstat[wave][r32] = l_run;
   }
   __syncthreads();
-  // 8 threads per query row, 16 columns each (a 32-column block = a lane pair)
-  const int qi = threadIdx.x >> 3, d0 = (threadIdx.x & 7) * 16;
+  // One query row per lane, 16 columns each: wavefront w takes the 32-column
+  // block w of every row, lanes l and l + 32 its two halves
+  static_assert(kAttnWaves * 32 == kAttnD, "one 32-column block per wavefront");
+  const int qi = lane & 31, d0 = 32 * wave + 16 * hf;
   const bool valid = q0 + qi < S;  // the pair exchange below needs both lanes
   float M = -INFINITY;
 #pragma unroll
@@ -808,7 +823,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     float a = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) a = fmaxf(a, fabsf(ov[j]));
-    const float amax = fmaxf(a, __shfl_xor(a, 1));
+    const float amax = fmaxf(a, __shfl_xor(a, 32));
     const float qinv = amax > 0.f ? __fdiv_rn(127.0f, amax) : 0.f;
     i32x4 codes;
 #pragma unroll
@@ -829,7 +844,7 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     } else {
       *reinterpret_cast<i32x4*>(sp.aq + row * args.out_stride + col) = codes;
     }
-    if ((threadIdx.x & 1) == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(amax, 127.0f);
+    if (hf == 0) sp.asc[row * (args.out_stride / 32) + col / 32] = __fdiv_rn(amax, 127.0f);
     return;
   }
   if (!valid) return;

@@ -102,6 +102,10 @@ struct GemmArgs {
   const QkvFuse* qf = nullptr;
   const float* qnw = nullptr;
   const float* knw = nullptr;
+  // kQkvNorm: q head tiles (128 columns each) before the k and v ones; with
+  // q_tiles and the k/v tile count multiples of 4, each XCD takes one half of
+  // the rows and a quarter of the KV groups (qkv_tile_of)
+  int qkv_q_tiles = 0;
   // kAccumNorm: norm weight and eps, codes [M][N] (tile-major when n_tiled)
   // and scales [M][N / 32] of the normalised rows (N = 256 P, P <= 4), the
   // band counters, and a flag that gets bit 2 if a helper's wait ran out

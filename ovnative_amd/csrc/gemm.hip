@@ -354,6 +354,29 @@ __device__ __forceinline__ bool band_tile_of(int id, int n_tiles, int m_tiles, i
   return mt < m_tiles;
 }
 
+// The q/k/v launch: XCD x takes row half x / 4 (m tiles below / from
+// ceil(m_tiles / 2)) and KV-group quarter g = x % 4: q head tiles
+// g Q/4 .. (g+1) Q/4 - 1, and the k and v tiles of KV heads g V/4 .. (g+1) V/4 - 1
+// (Q q tiles, V k tiles, V v tiles; Q % 4 == V % 4 == 0).  Workgroups are
+// dispatched to the XCDs round-robin (id % 8); XCD x walks its m tiles, each
+// as Q/4 + V/2 consecutive slots.  The attention launch after it gives XCD x
+// the tasks of segment x / 4 (two segments) and KV heads 2g, 2g + 1 (8 KV
+// heads), so with two segments of about half the rows each the q rows and
+// K/V planes it reads were written through its own L2.  Grid: 8 (Q/4 + V/2)
+// ceil(m_tiles / 2); slots past the XCD's last m tile return at once.
+__device__ __forceinline__ bool qkv_tile_of(int id, int q_tiles, int n_tiles, int m_tiles, int& nt,
+                                            int& mt) {
+  const int xcd = id & 7, slot = id >> 3;
+  const int qg = q_tiles >> 2, vg = (n_tiles - q_tiles) >> 3, per = qg + 2 * vg;
+  const int g = xcd & 3, mh = (m_tiles + 1) >> 1;
+  mt = (xcd >> 2) * mh + slot / per;
+  const int li = slot % per;
+  nt = li < qg ? g * qg + li
+               : (li < qg + vg ? q_tiles + g * vg + (li - qg)
+                               : q_tiles + 4 * vg + g * vg + (li - qg - vg));
+  return slot / per < mh && mt < m_tiles;
+}
+
 // NST-stage LDS ring (NST - 1 stages in flight), SB blocks per stage.  PIPE:
 // the stage loop runs as a software pipeline (below); without it each stage
 // is read, multiplied and folded block by block.
@@ -412,7 +435,9 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   const int n_tiles = (a.N + BN - 1) / BN;
   int ntile, mtile;
   if (MODE == kAccumNorm ? !band_tile_of(wg, n_tiles, (a.M + BM - 1) / BM, ntile, mtile)
-                         : !tile_of(wg, n_tiles, ntile, mtile))
+      : (MODE == kQkvNorm && a.qkv_q_tiles > 0)
+          ? !qkv_tile_of(wg, a.qkv_q_tiles, n_tiles, (a.M + BM - 1) / BM, ntile, mtile)
+          : !tile_of(wg, n_tiles, ntile, mtile))
     return;  // padding workgroup
   const int n0 = ntile * BN, m0 = mtile * BM;
   const int Kb = a.Kb;
@@ -1076,9 +1101,16 @@ template <int BM, bool PIPE, bool F16>
 hipError_t launch_qkv_cfg(const GemmArgs& a, hipStream_t st) {
   constexpr int BN = 128;
   const int64_t n_tiles = a.N / BN, m_tiles = ((int64_t)a.M + BM - 1) / BM;
-  const dim3 grid((unsigned)grid_size(n_tiles, m_tiles)), block(8 * BM);
+  const int64_t q_tiles = a.qkv_q_tiles, kv_tiles = n_tiles - q_tiles;
+  GemmArgs b = a;
+  // the XCD layout of qkv_tile_of where the head counts allow it
+  const bool halves = q_tiles > 0 && q_tiles % 4 == 0 && kv_tiles > 0 && kv_tiles % 8 == 0;
+  if (!halves) b.qkv_q_tiles = 0;
+  const dim3 grid((unsigned)(halves ? 8 * (q_tiles / 4 + kv_tiles / 4) * ((m_tiles + 1) / 2)
+                                    : grid_size(n_tiles, m_tiles))),
+      block(8 * BM);
   hipLaunchKernelGGL((gemm16_kernel<BN, BM, 4, BM / 32, 4, 2, kQkvNorm, PIPE, F16>), grid, block, 0,
-                     st, a);
+                     st, b);
   return hipGetLastError();
 }
 

@@ -945,6 +945,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         ga.qf = d_qf;
         ga.qnw = Y.qn;
         ga.knw = Y.kn;
+        ga.qkv_q_tiles = (int)(QD / 128);
         if (f16) {
           OVH_HIP(ovh::launch_widen_f16(aq, aq16, Tpad * ga.Kp, st), "widen codes");
           ga.W16 = Y.qkv->w.q16;
