@@ -386,6 +386,11 @@ void ovh_lm_set_graphs(OvhLm* lm, int on);
  * the same bits.  No reference counterpart (lm.cpp:339-401 runs the norm as a
  * step of its own). */
 void ovh_lm_set_fused_norm(OvhLm* lm, int on);
+/* L2 prefetch of o_proj's weight: 1 = the attention launch carries workgroups
+ * that load it into the L2 of every XCD that reads it, below 2048 rows and
+ * where they fit beside the attention's own workgroups (default), 0 = off.
+ * Nothing is written: both give the same bits.  No reference counterpart. */
+void ovh_lm_set_prefetch(OvhLm* lm, int on);
 /* LmRunnerSampleThunk (cuda_lm.h:39-41): the per-step guidance + argmax pass
  * (tts.cpp:296-326) on device logit planes; pred/scores host [C, target_len]. */
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,

@@ -86,6 +86,7 @@ SIGNATURES = {
     "ovh_lm_set_attention": (None, [_p, _int]),
     "ovh_lm_set_graphs": (None, [_p, _int]),
     "ovh_lm_set_fused_norm": (None, [_p, _int]),
+    "ovh_lm_set_prefetch": (None, [_p, _int]),
 }
 
 
@@ -642,6 +643,10 @@ class LM:
     def set_fused_norm(self, on: bool) -> None:
         """Run each RMSNorm after o_proj / down in the same launch (default) or as its own."""
         load().ovh_lm_set_fused_norm(self.handle, int(bool(on)))
+
+    def set_prefetch(self, on: bool) -> None:
+        """Prefetch o_proj's weight into L2 from the attention launch (default) or not."""
+        load().ovh_lm_set_prefetch(self.handle, int(bool(on)))
 
     def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
                target_len: int, guidance: float, layer_penalty: float):

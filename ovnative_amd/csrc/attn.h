@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
+#include "ovh_common.h"
+
 namespace ovh {
 
 constexpr int kAttnMaxSegs = 32;  // segments per attention launch
@@ -72,6 +74,9 @@ struct AttnSplit {
   int8_t* aq;
   float* asc;
   bool aq_tiled;  // codes tile-major (act_index), as the runner's GEMM reads them
+  // Optional: the next launch's weight into the L2s by extra workgroups
+  // (l2_prefetch; the runner passes the o_proj weight)
+  L2Prefetch pf;
 };
 // Splits K and V of the segments into the planes, then attends.
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,

@@ -526,6 +526,12 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
   _Float16* qs_h = reinterpret_cast<_Float16*>(&part[0][0][0]);
   _Float16* qs_l = qs_h + kAttnQ * kQPad;
 
+  // prefetch workgroups (sp.pf, sp.pf.wgs per XCD) follow the 8 * per_xcd
+  // attention workgroups
+  if ((int)blockIdx.x >= 8 * per_xcd) {
+    l2_prefetch(sp.pf, ((int)blockIdx.x - 8 * per_xcd) >> 3, (int)blockIdx.x & 7);
+    return;
+  }
   // XCD-aware task order: workgroups reach the 8 XCDs round-robin (id % 8);
   // XCD x takes the x-th contiguous range of tasks, and tasks are numbered
   // (segment, KV head, head in group, query tile)-major, so the two heads of a
@@ -1140,6 +1146,22 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
   }
 }
 
+namespace {
+// resident workgroups per CU of the short form: a property of the kernel on
+// the architecture
+template <bool kBits>
+int split_occupancy() {
+  static const int occ = [] {
+    int o = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, attention_split_kernel<kBits>, 256, 0) ==
+                   hipSuccess
+               ? o
+               : 0;
+  }();
+  return occ;
+}
+}  // namespace
+
 hipError_t launch_attention_split(const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                   hipStream_t st) {
   if (args.n_segs <= 0 || max_rows <= 0) return hipSuccess;
@@ -1185,17 +1207,21 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
                          qtiles, per_xcd);
     return hipGetLastError();
   }
-  // 1-D grid of 8 * per_xcd workgroups (XCD-aware task order in the kernel)
+  // 1-D grid of 8 * per_xcd workgroups (XCD-aware task order in the kernel),
+  // then the prefetch workgroups
   const int qtiles = (max_rows + kAttnQ - 1) / kAttnQ;
   const int tasks = args.n_segs * args.n_heads * qtiles;
   const int per_xcd = (tasks + 7) / 8;
-  const dim3 grid((unsigned)(8 * per_xcd));
-  if (mask_bits)
-    hipLaunchKernelGGL(attention_split_kernel<true>, grid, dim3(256), 0, st, args, sp, qtiles,
-                       per_xcd);
-  else
-    hipLaunchKernelGGL(attention_split_kernel<false>, grid, dim3(256), 0, st, args, sp, qtiles,
-                       per_xcd);
+  // the prefetch workgroups only where all of them are resident beside the
+  // attention's own (else they would run after them and lengthen the launch)
+  auto kernel = mask_bits ? attention_split_kernel<true> : attention_split_kernel<false>;
+  AttnSplit s = sp;
+  if (!s.pf.p || s.pf.bytes <= 0 || s.pf.wgs <= 0 ||
+      8 * (int64_t)(per_xcd + s.pf.wgs) >
+          (int64_t)(mask_bits ? split_occupancy<true>() : split_occupancy<false>()) * device_cus())
+    s.pf.wgs = 0;
+  const dim3 grid((unsigned)(8 * per_xcd + 8 * s.pf.wgs));
+  hipLaunchKernelGGL(kernel, grid, dim3(256), 0, st, args, s, qtiles, per_xcd);
   return hipGetLastError();
 }
 

@@ -203,6 +203,45 @@ __host__ __device__ inline int64_t grid_size(int64_t n_tiles, int64_t m_tiles) {
   return 8 * ((n_tiles + 7) / 8) * m_tiles;
 }
 
+// An L2 prefetch carried by a launch for the launch after it: `wgs` extra
+// workgroups per XCD, appended to the grid, load one dword of every 128-byte
+// line of `p` (all of it on every XCD, or with `slice` XCD x its eighth
+// [x bytes / 8, (x + 1) bytes / 8)) after `sleep` rounds of s_sleep 127 (~8k
+// clocks each, so that the launch's own first loads go first).  The lines stay
+// in the XCD's L2 across the launch boundary: the next launch's first reads of
+// its weight then hit there instead of HBM.  Nothing is written.
+struct L2Prefetch {
+  const int8_t* p = nullptr;
+  int64_t bytes = 0;
+  int wgs = 0;
+  int sleep = 0;
+  int slice = 0;
+};
+
+// Compute units of the current device (0 if the query fails).
+inline int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus;
+}
+
+// The body of prefetch workgroup j of XCD xcd (blockDim.x threads).
+__device__ __forceinline__ void l2_prefetch(const L2Prefetch& pf, int j, int xcd) {
+  for (int i = 0; i < pf.sleep; ++i) __builtin_amdgcn_s_sleep(127);
+  const int64_t lo = pf.slice ? pf.bytes * xcd / 8 : 0;
+  const int64_t hi = pf.slice ? pf.bytes * (xcd + 1) / 8 : pf.bytes;
+  const int64_t per = (hi - lo + pf.wgs - 1) / pf.wgs;
+  const int64_t b0 = lo + j * per, b1 = b0 + per < hi ? b0 + per : hi;
+  const int64_t stride = (int64_t)blockDim.x * 128;
+  uint32_t acc = 0;
+#pragma unroll 8
+  for (int64_t off = b0 + (int64_t)threadIdx.x * 128; off + 4 <= b1; off += stride)
+    acc ^= *reinterpret_cast<const uint32_t*>(pf.p + off);
+  asm volatile("" ::"v"(acc));  // the loads are kept (and waited for) without a store
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding; expcnt left alone): this
 // wavefront's DMA ops older than the last N have landed in LDS and its own LDS
 // reads have returned.

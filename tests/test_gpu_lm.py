@@ -457,6 +457,29 @@ def test_fused_norm_equals_separate_norm(small_lm, batch, seq):
     assert np.array_equal(got.view(np.int32), want.view(np.int32))
 
 
+@pytest.mark.parametrize("batch,seq", [(2, 300), (1, 600)])
+def test_prefetch_equals_no_prefetch(small_lm, batch, seq):
+    """The L2 prefetch workgroups (the attention launch loading o_proj's
+    weight) write nothing: the logits are the bits of the forward without
+    them, over graph replays and eager launches."""
+    ts, table, lm = small_lm
+    x = make_inputs(77 + seq, SMALL, batch, seq, min(12, seq // 3))
+    lm.set_prefetch(False)
+    try:
+        want = lm.forward(*x)
+    finally:
+        lm.set_prefetch(True)
+    for rep in range(3):
+        got = lm.forward(*x)
+        assert np.array_equal(got.view(np.int32), want.view(np.int32)), rep
+    lm.set_graphs(False)
+    try:
+        got = lm.forward(*x)
+    finally:
+        lm.set_graphs(True)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))
+
+
 # ---------------------------------------------------------------------------
 # BASELINE config 4 at full size: 28 layers, hidden 1024, 16/8 heads, inter
 # 3072, head 8 x 1025, the tts.cpp CFG batch B = 2, S = 300 (40 text + 260
