@@ -721,6 +721,21 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     constexpr int NT = 64 * NW;
     const QkvFuse& F = *reinterpret_cast<const QkvFuse*>(qkv_f);
     const int QD = F.QD, KVD = F.KVD;
+    // F's pointers are read from LDS, so the compiler cannot tell they point
+    // to global memory and would access through them with flat instructions,
+    // which also count in lgkmcnt: every later wait for an LDS read would then
+    // wait for the plane stores as well.  Global-qualified copies instead.
+    typedef __attribute__((address_space(1))) float gf32;
+    typedef __attribute__((address_space(1))) _Float16 gf16;
+    typedef __attribute__((address_space(1))) f32x4 gf32x4;
+    typedef __attribute__((address_space(1))) h8 gh8;
+    gf32* const Fq = (gf32*)F.q;
+    gf16* const Fkh = (gf16*)F.kh;
+    gf16* const Fkl = (gf16*)F.kl;
+    gf16* const Fvh = (gf16*)F.vh;
+    gf16* const Fvl = (gf16*)F.vl;
+    const gf32* const Fcos = (const gf32*)F.cos_tab;
+    const gf32* const Fsin = (const gf32*)F.sin_tab;
     float v[FN][FM][4];
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
@@ -755,13 +770,13 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
           const int64_t kb = F.vt_off[sg] / 32 + p / 32;
           if (is_v) {
             const int64_t at = v_tile_index(kvh, F.nkb, kb, p & 31, c);
-            F.vh[at] = (_Float16)0.f;
-            F.vl[at] = (_Float16)0.f;
+            Fvh[at] = (_Float16)0.f;
+            Fvl[at] = (_Float16)0.f;
           } else {
             const int64_t at = k_tile_index(kvh, F.nkb, kb, p & 31, 8 * c);
             const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-            *reinterpret_cast<h8*>(F.kh + at) = z;
-            *reinterpret_cast<h8*>(F.kl + at) = z;
+            *reinterpret_cast<gh8*>(Fkh + at) = z;
+            *reinterpret_cast<gh8*>(Fkl + at) = z;
           }
         }
       }
@@ -784,8 +799,8 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
             _Float16 hi, lo;
             split16(x, hi, lo);
             const int64_t at = v_tile_index(kvh, F.nkb, kb, p & 31, wn * 32 + i * 16 + 4 * q + e);
-            F.vh[at] = hi;
-            F.vl[at] = lo;
+            Fvh[at] = hi;
+            Fvl[at] = lo;
           }
       }
       zero_pad(true, kvh);
@@ -812,8 +827,8 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) x[i] = xs[row][jj + 8 * i];
-      norm_rope_lanes8(x, is_q ? a.qnw : a.knw, F.cos_tab + r * (kHeadD / 2),
-                       F.sin_tab + r * (kHeadD / 2), F.eps, jj);
+      norm_rope_lanes8(x, is_q ? a.qnw : a.knw, Fcos + r * (kHeadD / 2), Fsin + r * (kHeadD / 2),
+                       F.eps, jj);
       // each lane writes back exactly the elements it read
 #pragma unroll
       for (int i = 0; i < 16; ++i) xs[row][jj + 8 * i] = x[i];
@@ -825,7 +840,7 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
         const int c = threadIdx.x + NT * t, row = c >> 5, col = (c & 31) * 4;
         const int64_t r = m0 + row;
         if (r < a.M)
-          *reinterpret_cast<f32x4*>(F.q + r * QD + n0 + col) =
+          *reinterpret_cast<gf32x4*>(Fq + r * QD + n0 + col) =
               *reinterpret_cast<const f32x4*>(&xs[row][col]);
       }
       return;
@@ -849,8 +864,8 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
         ll[e] = lo;
       }
       const int64_t at = k_tile_index(kvh, F.nkb, kb, p & 31, 8 * g);
-      *reinterpret_cast<h8*>(F.kh + at) = hh;
-      *reinterpret_cast<h8*>(F.kl + at) = ll;
+      *reinterpret_cast<gh8*>(Fkh + at) = hh;
+      *reinterpret_cast<gh8*>(Fkl + at) = ll;
     }
     zero_pad(false, kvh);
     if (bad) atomicOr(F.overflow, 1u);

@@ -37,11 +37,11 @@ __device__ __forceinline__ int64_t v_tile_index(int kvh, int64_t nkb, int64_t kb
 // fma chain j, and both members of the rotation pairs (j + 8i, j + 8i + 64),
 // i < 8.  The chain runs in registers, the 8 chain sums are added left to right
 // after 7 lane reads; then xn = (x * scale) * w and the rotation
-// fmsub(na, c, nb s) / fmadd(na, s, nb c) with the row's cos/sin tables.
+// fmsub(na, c, nb s) / fmadd(na, s, nb c) with the row's cos/sin tables (TP:
+// a pointer to const float, in any address space).
+template <typename TP>
 __device__ __forceinline__ void norm_rope_lanes8(float (&x)[16], const float* __restrict__ w,
-                                                 const float* __restrict__ cos_row,
-                                                 const float* __restrict__ sin_row, float eps,
-                                                 int j) {
+                                                 TP cos_row, TP sin_row, float eps, int j) {
   constexpr int D = kHeadD, half = D / 2;
   float s = 0.f;
 #pragma unroll
