@@ -507,6 +507,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_split_kernel(
 // the K and V fragments of its next block while it computes the current one.
 constexpr int kQPad = kAttnD + 8;  // LDS row of a Q plane, in halves
 constexpr int kPartRow = kAttnD + 4;  // LDS row of a merge partial, in floats
+// The split forms' lazy softmax reference: a row's exponents are taken
+// against a value at most this far (base 2) below its largest score so far.
+constexpr float kLazyLog2 = 8.0f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kMaskedLog2 = -1e29f * kLog2e;
 
@@ -683,7 +686,8 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
     // base-2 units
     float bv[16];
     if (kBits) {
-      if (has_bits) {
+      // every key of every lane visible (most blocks): no bias, the same bits
+      if (has_bits && !__all((mword & 0x0F0F0F0Fu) == 0x0F0F0F0Fu)) {
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
@@ -715,7 +719,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
 #pragma unroll
     for (int e = 0; e < 16; ++e)
       p[e] = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
-    if (t0 + kAttnK > S) {  // keys past the segment (uniform: the last block only)
+    // keys past the segment: the partial block, if any, is the last one the
+    // wavefront takes (uniform)
+    if (!decltype(next)::value && t0 + kAttnK > S) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         if (t0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= S) p[e] = -INFINITY;
@@ -723,9 +729,12 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
 #pragma unroll
     for (int e = 0; e < 16; ++e) bmax = fmaxf(bmax, p[e]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float m_new = fmaxf(m_run, bmax);
+    // The row's reference m_run (the exponents are taken against it) moves
+    // only when a score exceeds it by more than kLazyLog2, so p <= 2^kLazyLog2;
+    // then the output and the sum are rescaled, in most blocks not at all.
+    const bool up = bmax > m_run + kLazyLog2;
+    const float m_new = up ? bmax : m_run;
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;  // all keys so far at -inf
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     float psum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -733,22 +742,25 @@ __global__ __launch_bounds__(256, 2) void attention_split_kernel(AttnArgs args, 
       psum = __fadd_rn(psum, p[e]);
     }
     psum = __fadd_rn(psum, __shfl_xor(psum, 32));
+    // a row that keeps its reference gets alpha = 1: l_run + psum, o unchanged
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     l_run = fmaf(l_run, alpha, psum);
-    m_run = m_new;
-
-    if (hf == 0) alpha_s[wave][r32] = alpha;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (__any(up)) {  // uniform
+      if (hf == 0) alpha_s[wave][r32] = alpha;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&alpha_s[wave][8 * g + 4 * hf]);
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&alpha_s[wave][8 * g + 4 * hf]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+          for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
+    m_run = m_new;
 
     // ---- O += P V: 16-key chunk c takes this lane's p[8c .. 8c+7]
 #pragma unroll
@@ -1003,7 +1015,8 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
     float bv[16];
     if (kBits) {
       const uint32_t mword = mword_raw >> (4 * hf);
-      if (has_bits) {
+      // every key of every lane visible (most blocks): no bias, the same bits
+      if (has_bits && !__all((mword & 0x0F0F0F0Fu) == 0x0F0F0F0Fu)) {
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           bv[e] = mword & (1u << (8 * (e >> 2) + (e & 3))) ? 0.f : kMaskedBias;
@@ -1021,7 +1034,9 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
 #pragma unroll
     for (int e = 0; e < 16; ++e)
       p[e] = (kBits || brow) ? fmaf(st[e], sl2, bv[e]) : __fmul_rn(st[e], sl2);
-    if (t0 + kAttnK > S) {  // keys past the segment (uniform: the last block only)
+    // keys past the segment: the partial block, if any, is the last one the
+    // wavefront takes (uniform)
+    if (!decltype(next)::value && t0 + kAttnK > S) {
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         if (t0 + 8 * (e >> 2) + 4 * hf + (e & 3) >= S) p[e] = -INFINITY;
@@ -1029,9 +1044,10 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
 #pragma unroll
     for (int e = 0; e < 16; ++e) bmax = fmaxf(bmax, p[e]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float m_new = fmaxf(m_run, bmax);
+    // lazy reference, as in attention_split_kernel
+    const bool up = bmax > m_run + kLazyLog2;
+    const float m_new = up ? bmax : m_run;
     const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     float psum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -1039,22 +1055,25 @@ __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs ar
       psum = __fadd_rn(psum, p[e]);
     }
     psum = __fadd_rn(psum, __shfl_xor(psum, 32));
+    // a row that keeps its reference gets alpha = 1: l_run + psum, o unchanged
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
     l_run = fmaf(l_run, alpha, psum);
-    m_run = m_new;
-
-    if (hf == 0) xs[wave][r32] = alpha;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (__any(up)) {  // uniform
+      if (hf == 0) xs[wave][r32] = alpha;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&xs[wave][8 * g + 4 * hf]);
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(&xs[wave][8 * g + 4 * hf]);
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+          for (int e = 0; e < 4; ++e) o[c][4 * g + e] = __fmul_rn(o[c][4 * g + e], a4[e]);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
+    m_run = m_new;
 
     // ---- O += P V
     const _Float16* vb = kb + 2 * kLdsPlane;
