@@ -424,7 +424,7 @@ def test_linear_q_grouped_errors(oracle):
 # ---------------------------------------------------------------------------
 # fused producers at LM shapes vs the oracle
 
-@pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (40, 256), (7, 512),
+@pytest.mark.parametrize("M,K", [(600, 1024), (128, 1024), (1, 1024), (40, 256), (7, 512), (4099, 1024),
                                  (9, 768), (13, 100), (5, 1280)])
 def test_rmsnorm_quantize_vs_oracle(oracle, M, K):
     import ovnative_amd as ov
