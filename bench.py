@@ -1066,7 +1066,9 @@ def main():
         "roofline": roofline_entry(
             "gemm16 residual + norm (o_proj K=2048 and down K=3072; M=600, N=1024, += x, then "
             "RMSNorm + quantise of the updated rows in the same launch), launched as the step "
-            "launches it: graph replay, tile-major codes, weights cold from HBM",
+            "launches it: graph replay, tile-major codes, weights cold from HBM (as the step's "
+            "down launches read theirs; its o_proj launches find their weight prefetched into "
+            "L2 by the attention launch and run ~2.5 us shorter)",
             rs["ops"], residual_bytes(cfg, M) + norm_out_bytes(cfg, M), rs["graph_norm_ms"],
             residual_traffic(NORM_TRAFFIC),
             avg_ms_plain_residual=round(rs["graph_ms"], 5),
