@@ -116,17 +116,23 @@ def log(msg: str) -> None:
 def make_checkpoint(cfg: dict, seed: int = 0):
     """Random int8 checkpoint with the reference's tensor names and encodings
     (linears int8 [N, K] + per-row scales, embeddings int8 + per-row scales,
-    fp32 norms); generated on the GPU, returned as host arrays."""
+    fp32 norms): fp32 weights drawn on the GPU, quantised on the host by
+    ovw1.quantize_int8 (the converter's quantisation, tools/convert_weights.py:
+    130-135), returned as host arrays."""
     import numpy as np
     import torch
     from ovnative_amd import ovw1
     g = torch.Generator(device="cuda").manual_seed(seed)
 
     def q8(rows, cols):
-        w = torch.randn((rows, cols), generator=g, device="cuda") * 0.02
-        s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-12)
-        q = torch.clamp(torch.round(w / s[:, None]), -127, 127).to(torch.int8)
-        return q.cpu().numpy(), s.float().cpu().numpy()
+        qs, ss = [], []
+        for r0 in range(0, rows, 16384):  # row chunks bound the host temporaries
+            n = min(16384, rows - r0)
+            w = (torch.randn((n, cols), generator=g, device="cuda") * 0.02).cpu().numpy()
+            q, s = ovw1.quantize_int8(w)
+            qs.append(q)
+            ss.append(s)
+        return np.concatenate(qs), np.concatenate(ss)
 
     def norm(n):
         return (1.0 + 0.1 * torch.randn(n, generator=g, device="cuda")).float().cpu().numpy()

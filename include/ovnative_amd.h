@@ -137,12 +137,16 @@ int ovh_linear_q_tiled(int64_t M, const int8_t* aq, const float* asc, const OvhW
  * the bits of those two calls.  N = 256 P with P <= 4, K a multiple of 128.
  * band_cnt: ovh_band_counter_bytes(R) of device memory, R >= M, zeroed by
  * the caller before its first use, then passed unchanged to every later call
- * on that device with the same N (each launch advances its counters); calls
- * sharing one run in stream order.  Its first 4 bytes turn non-zero if a
- * workgroup's wait for the rest of its row band ran out (only possible
- * when other work keeps the device from holding the band's workgroups); the
- * outputs of that call are then not to be used.  No reference counterpart as
- * one call (the LM runner's o_proj / down launch). */
+ * on that device (each launch moves its counters on to the next launch
+ * boundary, whatever its N); calls sharing one run in stream order.  Its first
+ * 4 bytes turn non-zero if the row bands' hand-off failed: bit 1 (value 2) a
+ * workgroup's wait for the rest of its band ran out (only possible when other
+ * work keeps the device from holding the band's workgroups) or a counter was
+ * not at a launch boundary; bit 2 (value 4) a workgroup ran on another XCD
+ * than its band's.  The outputs of that call are then not to be used (the
+ * same result comes from ovh_linear_q_tiled + ovh_rmsnorm_quantize).  Needs a
+ * device of 8 XCDs (MI355X), else OV_ERR_NOT_IMPLEMENTED.  No reference
+ * counterpart as one call (the LM runner's o_proj / down launch). */
 int ovh_linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
                       int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
                       void* band_cnt, void* stream);
@@ -188,12 +192,23 @@ int ovh_linear(int64_t M, const float* A, const OvhWeight* w, float* C, int64_t 
  * and a widened copy of the codes per call.  Process-wide; returns the
  * previous setting (negative rows: unchanged, a query). */
 int64_t ovh_set_f16_min_rows(int64_t rows);
+/* The split-f16 attention's two kernels (ovh_attention_split and the LM
+ * runner): from `tasks` long-form workgroups on (segments x KV heads x 128-row
+ * query tiles; default 384, 0 = whenever 4 % (n_heads / n_kv_heads) == 0) the
+ * long-sequence kernel, which shares each key block through LDS, else the
+ * short one, which splits the keys over four wavefronts and merges.  Both are
+ * within the operator's tolerance of the reference; they sum in another
+ * order, so a batch and its requests run alone give the same bits only when
+ * they take the same kernel.  No reference counterpart (the CUDA runner picks
+ * its attention kernel from the sequence length, cuda_lm.cu:1106-1115).
+ * Process-wide; returns the previous setting (negative: unchanged, a query). */
+int64_t ovh_set_attention_long_min_tasks(int64_t tasks);
 /* ovh_linear without any allocation: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The codes and scales
  * go to a fixed 16 MiB device array per GPU (held from the first call on that
  * GPU until the process ends), so M * (Kp + 4 * Kb) plus up to 255 bytes of
- * alignment must fit in 16 MiB (e.g. M <= 14560 at K = 1024, M <= 4850 at
+ * alignment must fit in 16 MiB (M <= 14563 at K = 1024, M <= 4854 at
  * K = 3072); larger calls return OV_ERR_INVALID_ARG.  Every call on one GPU
  * shares that array: calls that overlap on one GPU (other streams, other
  * threads) race; order them on one stream.  Same results, bit for bit, as
@@ -396,6 +411,50 @@ void ovh_lm_set_prefetch(OvhLm* lm, int on);
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,
                   int target_len, float guidance, float layer_penalty, int32_t* pred,
                   float* scores);
+/* In-runner recovery, as the CUDA runner's forward falls back to its cuBLAS
+ * path when the fused attention cannot run (cuda_lm.cu:586-606, :620-622).
+ * Two conditions that only a finished forward shows make the default kernels'
+ * results unusable: |k| or |v| beyond the f16 range of the split-f16
+ * attention, and a fused residual + norm launch whose row-band hand-off failed
+ * (ovh_linear_q_norm's error bits).  Wherever the runner synchronises with the
+ * host (ovh_lm_forward with host logits, ovh_lm_forward_cfg, ovh_lm_sample on
+ * the last forward's own logits, hence every step of ovh_lm_generate) it
+ * checks for them, runs that forward again on the exact fallback (the fp32
+ * attention form, the norm as a launch of its own: the bits those settings
+ * give when chosen from the start), keeps the fallback for later forwards,
+ * and returns OV_OK.  ovh_lm_recovered: the fallbacks taken so far, a mask of
+ * OVH_LM_RECOVERED_*.  No reference counterpart as a call. */
+#define OVH_LM_RECOVERED_ATTENTION 1
+#define OVH_LM_RECOVERED_NORM 2
+int ovh_lm_recovered(const OvhLm* lm);
+/* The conditions behind the last recovery (0 if none): bit 0 (value 1) the
+ * attention's inputs beyond f16, bit 1 (2) a band's hand-off wait ran out or
+ * its counter was off a launch boundary, bit 2 (4) a workgroup of the fused
+ * norm launch on another XCD than its band's. */
+int ovh_lm_last_flags(const OvhLm* lm);
+/* Test support: force a condition the recovery handles on the next forward,
+ * from the host, with every kernel still ending normally.
+ * OVH_LM_FORCE_BAND_WAIT puts the first row band's counter off its launch
+ * boundary (the hand-off reports it, and that band's bounded waits run out);
+ * OVH_LM_FORCE_XCD makes every fused launch's XCD placement check fail.
+ * No reference counterpart. */
+#define OVH_LM_FORCE_BAND_WAIT 1
+#define OVH_LM_FORCE_XCD 2
+void ovh_lm_force_condition(OvhLm* lm, int what);
+/* Stage timer, as the reference's OV_CUDA_PROFILE events (cuda_lm.cu:994-1022,
+ * :1036-1197): with on = 1 each forward launches its kernels one by one with
+ * HIP events between the stages and waits for them; ovh_lm_stage_times then
+ * gives the last forward's milliseconds per stage, summed over the layers
+ * (ms[i], i < n), and the stage labels (names[i] if names is not NULL), and
+ * returns the number of stages.  Stages: "prep+embed" (input upload, masks,
+ * embedding), "qkv" (the q/k/v GEMM with qk-norm and RoPE), "attn", "o_proj"
+ * (with the norm after it when fused), "gate_up" (with SiLU), "down" (with
+ * the next norm when fused), "final_norm+head"; a norm that runs as a launch
+ * of its own counts with the stage after it, as in the reference.  The
+ * environment variable OVH_LM_PROFILE, set when the runner is created, turns
+ * it on and prints one "[hip-stage]" line per forward to stderr. */
+void ovh_lm_set_profile(OvhLm* lm, int on);
+int ovh_lm_stage_times(const OvhLm* lm, double* ms, const char** names, int n);
 
 /* ---- the CFG decoding loop ----------------------------------------------- */
 

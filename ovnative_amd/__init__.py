@@ -58,6 +58,7 @@ SIGNATURES = {
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
     "ovh_set_f16_min_rows": (_i64, [_i64]),
+    "ovh_set_attention_long_min_tasks": (_i64, [_i64]),
     "ovh_copy_last_error": (C.c_size_t, [C.c_char_p, C.c_size_t]),
     "ovh_linear_q_grouped": (_int, [_p, _int, _int, _p]),
     "ovh_weight_gate_up": (_int, [_p, _p, _p, C.POINTER(_p)]),
@@ -87,7 +88,16 @@ SIGNATURES = {
     "ovh_lm_set_graphs": (None, [_p, _int]),
     "ovh_lm_set_fused_norm": (None, [_p, _int]),
     "ovh_lm_set_prefetch": (None, [_p, _int]),
+    "ovh_lm_recovered": (_int, [_p]),
+    "ovh_lm_last_flags": (_int, [_p]),
+    "ovh_lm_force_condition": (None, [_p, _int]),
+    "ovh_lm_set_profile": (None, [_p, _int]),
+    "ovh_lm_stage_times": (_int, [_p, _p, _p, _int]),
 }
+
+# ovh_lm_recovered bits and ovh_lm_force_condition conditions (ovnative_amd.h)
+RECOVERED_ATTENTION, RECOVERED_NORM = 1, 2
+FORCE_BAND_WAIT, FORCE_XCD = 1, 2
 
 
 class GenOptions(C.Structure):
@@ -388,6 +398,13 @@ def set_f16_min_rows(rows: int) -> int:
     return int(load().ovh_set_f16_min_rows(int(rows)))
 
 
+def set_attention_long_min_tasks(tasks: int) -> int:
+    """ovh_set_attention_long_min_tasks: from how many long-form workgroups the
+    split attention takes its long-sequence kernel (default 384; 0: whenever
+    the head grouping allows it); returns the previous setting."""
+    return int(load().ovh_set_attention_long_min_tasks(int(tasks)))
+
+
 def linear_q_sliced(aq, asc, w: Weight, slice_n, outs=None):
     """One launch over a concatenated weight, one output per slice (gemm.cpp:776-827)."""
     torch = _torch()
@@ -647,6 +664,32 @@ class LM:
     def set_prefetch(self, on: bool) -> None:
         """Prefetch o_proj's weight into L2 from the attention launch (default) or not."""
         load().ovh_lm_set_prefetch(self.handle, int(bool(on)))
+
+    def recovered(self) -> int:
+        """Fallbacks the runner took after a forward's flags (RECOVERED_* bits)."""
+        return load().ovh_lm_recovered(self.handle)
+
+    def last_flags(self) -> int:
+        """The condition bits behind the last recovery (ovh_lm_last_flags)."""
+        return load().ovh_lm_last_flags(self.handle)
+
+    def force_condition(self, what: int) -> None:
+        """Test support: force FORCE_BAND_WAIT / FORCE_XCD on the next forward."""
+        load().ovh_lm_force_condition(self.handle, int(what))
+
+    def set_profile(self, on: bool) -> None:
+        """Stage timer on (eager launches with HIP events between stages) or off."""
+        load().ovh_lm_set_profile(self.handle, int(bool(on)))
+
+    def stage_times(self) -> dict:
+        """The last profiled forward's milliseconds per stage, in stage order."""
+        lib = load()
+        n = lib.ovh_lm_stage_times(self.handle, None, None, 0)
+        ms = (C.c_double * max(n, 1))()
+        names = (C.c_char_p * max(n, 1))()
+        n = lib.ovh_lm_stage_times(self.handle, C.cast(ms, C.c_void_p), C.cast(names, C.c_void_p),
+                                   n)
+        return {names[i].decode(): float(ms[i]) for i in range(n)}
 
     def sample(self, cond_ptr: int, cond_seq: int, uncond_ptr: int, uncond_seq: int,
                target_len: int, guidance: float, layer_penalty: float):

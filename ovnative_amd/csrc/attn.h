@@ -94,4 +94,8 @@ hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const 
                                      const AttnArgs& args, const AttnSplit& sp, int max_rows,
                                      hipStream_t st);
 
+// From how many long-form workgroups (segments x KV heads x 128-row query
+// tiles) the split attention takes its long-sequence kernel; process-wide.
+int64_t attention_long_min_tasks();
+void set_attention_long_min_tasks(int64_t tasks);
 }  // namespace ovh

@@ -1,5 +1,6 @@
 // Attention side of one decoder layer for gfx950: RoPE tables, fused per-head
 // RMSNorm + RoPE, and bidirectional GQA attention with an additive bias.
+#include <atomic>
 #include <cstdint>
 #include <type_traits>
 
@@ -895,6 +896,8 @@ constexpr int kLdsPlane = 32 * kAttnD;  // halves per plane per block
 // 8 x 300 39.5 / 41.7 (320), 4 x 768 87.6 / 80.4 (384), 2 x 1024 76.3 / 73.3
 // (256), 8 x 512 86.0 / 65.7 (512), 16 x 300 73.7 / 63.0 (640).
 constexpr int kLdsMinTasks = 384;
+// The threshold in use (ovh_set_attention_long_min_tasks), process-wide.
+std::atomic<int64_t> g_long_min_tasks{kLdsMinTasks};
 
 template <bool kBits>
 __global__ __launch_bounds__(256, 2) void attention_split_lds_kernel(AttnArgs args, AttnSplit sp,
@@ -1211,7 +1214,7 @@ hipError_t launch_attention_split_only(const AttnArgs& args, const AttnSplit& sp
   const int QT = lds_ok ? kAttnWaves * kAttnQ / args.group : 1;  // query rows per long-form workgroup
   const int lds_qtiles = (max_rows + QT - 1) / QT;
   const int lds_tasks = lds_ok ? args.n_segs * (args.n_heads / args.group) * lds_qtiles : 0;
-  if (lds_ok && lds_tasks >= kLdsMinTasks) {
+  if (lds_ok && lds_tasks >= g_long_min_tasks.load(std::memory_order_relaxed)) {
     // a chip's worth of long-form workgroups: K/V blocks shared through LDS
     // by 128 query-head rows
     const int qtiles = lds_qtiles;
@@ -1259,6 +1262,11 @@ hipError_t launch_qk_norm_rope_split(float* q, float* k, const float* qw, const 
                      st, q, k, qw, kw, rows, n_heads, cos_tab, sin_tab, eps, q_blocks, ktiles,
                      args, sp);
   return hipGetLastError();
+}
+
+int64_t attention_long_min_tasks() { return g_long_min_tasks.load(std::memory_order_relaxed); }
+void set_attention_long_min_tasks(int64_t tasks) {
+  g_long_min_tasks.store(tasks, std::memory_order_relaxed);
 }
 
 }  // namespace ovh

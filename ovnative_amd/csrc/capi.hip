@@ -246,13 +246,16 @@ int linear_q(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, 
 
 int linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
                   int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
-                  unsigned long long* band_cnt, uint32_t* err, hipStream_t st) {
+                  unsigned long long* band_cnt, uint32_t* err, hipStream_t st, int xcd_test) {
   if (M <= 0) return OV_OK;
   int rc = check_gemm_operands(M, aq, asc, w);
   if (rc != OV_OK) return rc;
   if (!x || !nw || !nq || !nsc || !band_cnt || !err)
     return fail(OV_ERR_INVALID_ARG, "residual + norm GEMM: null operand");
   if (ldx < w->w.N) return fail(OV_ERR_INVALID_ARG, "ldx < N");
+  if (!ovh::norm_fusable())
+    return fail(OV_ERR_NOT_IMPLEMENTED,
+                "residual + norm GEMM: needs a device of 8 XCDs (the row bands' placement)");
   ovh::GemmArgs a = base_args(M, aq, asc, w);
   a.a_tiled = 1;
   a.nslices = 1;
@@ -267,6 +270,7 @@ int linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight
   a.n_tiled = 1;
   a.band_cnt = band_cnt;
   a.norm_err = err;
+  a.xcd_test = xcd_test;
   OVH_HIP(ovh::launch_gemm(a, ovh::kAccumNorm, st), "residual + norm gemm launch");
   return OV_OK;
 }
@@ -608,15 +612,16 @@ int ovh_linear_q_grouped(const OvhGemmGroup* groups, int n_groups, int accumulat
 
 namespace {
 // ovh_linear's quantised copy of A.  One workspace per (device, stream), kept
-// from the first call on that stream until the process ends and grown when a
-// call needs more: calls on one stream are ordered by the stream, calls on
-// different streams never share one.  Growth frees the old buffer and
+// from the first eager call on that stream until the process ends and grown
+// when a call needs more: eager calls on one stream are ordered by the stream,
+// calls on different streams never share one.  Growth frees the old buffer and
 // allocates the new one on the calling stream (hipFreeAsync/hipMallocAsync),
-// after that stream's earlier work.  Under graph capture a call that does not
-// fit the workspace allocates and frees in the graph instead, leaving the
-// workspace as it is.  A stream destroyed while a call on it is still running
-// must not be replaced by a new stream of the same handle before that call
-// ends.
+// after that stream's earlier work.  A call under graph capture never touches
+// the workspace: it allocates and frees in the graph (memory nodes), so the
+// graph owns its buffer, stays valid when a later eager call grows (frees)
+// the workspace, and shares nothing with eager calls or with replays on other
+// streams.  A stream destroyed while a call on it is still running must not be
+// replaced by a new stream of the same handle before that call ends.
 struct LinearWorkspace {
   int device;
   hipStream_t stream;
@@ -638,6 +643,12 @@ int linear_workspace(hipStream_t st, size_t bytes, void** ptr, bool* owned) {
   OVH_HIP(hipGetDevice(&dev), "hipGetDevice");
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   OVH_HIP(hipStreamIsCapturing(st, &cap), "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone) {
+    // the graph's own buffer (see above)
+    OVH_HIP(hipMallocAsync(ptr, bytes, st), "hipMallocAsync(linear workspace, captured)");
+    *owned = true;
+    return OV_OK;
+  }
   std::lock_guard<std::mutex> lock(g_ws_mu);
   LinearWorkspace* ws = nullptr;
   for (int i = 0; i < g_ws_n; ++i)
@@ -646,7 +657,7 @@ int linear_workspace(hipStream_t st, size_t bytes, void** ptr, bool* owned) {
     *ptr = ws->ptr;
     return OV_OK;
   }
-  if (cap != hipStreamCaptureStatusNone || (!ws && g_ws_n == kMaxLinearWorkspaces)) {
+  if (!ws && g_ws_n == kMaxLinearWorkspaces) {
     OVH_HIP(hipMallocAsync(ptr, bytes, st), "hipMallocAsync(linear workspace)");
     *owned = true;
     return OV_OK;
@@ -798,6 +809,12 @@ int ovh_linear_noalloc(int64_t M, const float* A, const OvhWeight* w, float* C, 
 int64_t ovh_set_f16_min_rows(int64_t rows) {
   const int64_t prev = ovh::f16_min_rows();
   if (rows >= 0) ovh::set_f16_min_rows(rows);
+  return prev;
+}
+
+int64_t ovh_set_attention_long_min_tasks(int64_t tasks) {
+  const int64_t prev = ovh::attention_long_min_tasks();
+  if (tasks >= 0) ovh::set_attention_long_min_tasks(tasks);
   return prev;
 }
 

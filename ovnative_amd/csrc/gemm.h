@@ -26,10 +26,30 @@ enum GemmMode {
 // band's counter once its stores are in that XCD's L2, and the last
 // GemmArgs::n_helpers to arrive (the launcher picks up to kMaxNormHelpers)
 // wait for the count to complete and normalise the band's rows.  The
-// counters are 64-bit, kBandCntStride words apart, zero when allocated, and
-// advance by the number of column tiles per launch.
-constexpr int kMaxNormHelpers = 32;
-constexpr int kBandCntStride = 32;
+// counters are 64-bit, one 512-byte slot (kBandCntStride words) per band,
+// zero when allocated.  A launch's arrivals at a band start at a multiple of
+// kBandRound, and the band's last arrival moves the counter on to the next
+// multiple, so a counter buffer serves launches of any column-tile count in
+// any order.  Words 1 .. 32 of a slot are the tags of the band's column
+// tiles: each workgroup writes (launch boundary << 4 | its XCC_ID) there
+// before it counts itself, and the helpers check, once the count is
+// complete, that every tile's tag is this launch's and names their own XCD.
+// Error bits of GemmArgs::norm_err: kNormErrWait, a band's wait ran out or
+// its counter was not at a launch boundary; kNormErrXcd, a tile of the band
+// ran on another XCD than its helpers (its rows may then have been
+// normalised from stale values).  The launch's outputs are not to be used
+// when either is set.
+constexpr int kMaxNormHelpers = 16;
+constexpr int kBandCntStride = 64;
+constexpr int kMaxBandTiles = 32;
+constexpr unsigned long long kBandRound = 1ull << 16;
+constexpr uint32_t kNormErrWait = 2u, kNormErrXcd = 4u;
+// XCDs the band placement assumes (workgroup id % 8 -> one XCD per residue:
+// the dispatcher hands workgroups to the XCDs round-robin, from an XCD that
+// differs between direct and graph launches), and whether the current device
+// has them: the fused norm is only launched where it does.
+constexpr int kBandXcds = 8;
+bool norm_fusable();
 // Counter slots: the 32-row bands of launches below 2048 rows take slots
 // 0 .. 63, the 64-row bands from 2048 rows slots kLargeMBandBase on.
 constexpr int kLargeMBandBase = 64;
@@ -108,7 +128,7 @@ struct GemmArgs {
   int qkv_q_tiles = 0;
   // kAccumNorm: norm weight and eps, codes [M][N] (tile-major when n_tiled)
   // and scales [M][N / 32] of the normalised rows (N = 256 P, P <= 4), the
-  // band counters, and a flag that gets bit 2 if a helper's wait ran out
+  // band counters, and the error word (kNormErrWait, kNormErrXcd)
   const float* nw = nullptr;
   float neps = 0.f;
   int8_t* nq = nullptr;
@@ -117,6 +137,10 @@ struct GemmArgs {
   unsigned long long* band_cnt = nullptr;
   uint32_t* norm_err = nullptr;
   int n_helpers = 8;  // set by the launcher
+  // kAccumNorm test support: non-zero makes the odd column tiles' tags name
+  // another XCD, so the helpers' placement check fails (the condition forced
+  // from the host; every workgroup still ends normally).  0 in use.
+  int xcd_test = 0;
 };
 
 // fp32 linear on the f16 matrix cores (gemm_f32.hip).  Weight: hi/lo f16

@@ -969,35 +969,58 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
   if constexpr (MODE == kAccumNorm) {
     // The band hand-off.  Once vmcnt has drained, this workgroup's result
     // stores are in the XCD's L2, where the band's counter add is performed
-    // after them (atomics execute in L2; the counter's 256-byte line is this
+    // after them (atomics execute in L2; the counter's 512-byte slot is this
     // band's alone, so no other XCD holds it).
     static_assert(BM % 32 == 0, "bands of whole 32-row block tiles");
     static_assert(NW * kRmsRowLds<4> * 4 + 16 <= NST * STAGE, "the row norm's LDS fits in the ring");
-    wait_vm_lgkm<0>();
-    __syncthreads();  // every wavefront's stores drained; the ring is free
     unsigned long long* const cnt = a.band_cnt + (int64_t)mtile * kBandCntStride;
     unsigned long long* const bc = reinterpret_cast<unsigned long long*>(&smem[0][0]);
+    const unsigned long long nt = (unsigned long long)n_tiles;  // <= kMaxBandTiles (host)
+    // XCC_ID: hardware register 20, bits 0-3
+    const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11));
+    // the tile's tag (bit 4: written in this launch; the XCD it ran on), in L2
+    // with the tile's result before the count
     if (threadIdx.x == 0)
-      bc[0] = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt + 1 + ntile,
+                         16ull | (unsigned long long)(xcc ^ ((a.xcd_test && (ntile & 1)) ? 1 : 0)),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vm_lgkm<0>();
+    __syncthreads();  // every wavefront's stores drained; the ring is free
+    if (threadIdx.x == 0) {
+      const unsigned long long v0 =
+          __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the band's last arrival moves the counter on to the next launch
+      // boundary (nothing of this launch arrives after it)
+      if (v0 % kBandRound == nt - 1)
+        __hip_atomic_fetch_add(cnt, kBandRound - nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bc[0] = v0;
+    }
     __syncthreads();
-    const unsigned long long v = bc[0], nt = (unsigned long long)n_tiles;
+    const unsigned long long v = bc[0];
     const unsigned long long helpers =
         nt < (unsigned long long)a.n_helpers ? nt : (unsigned long long)a.n_helpers;
-    const unsigned long long arrived = v % nt;  // this launch's arrivals before this one
+    const unsigned long long arrived = v % kBandRound;  // this launch's arrivals before this one
+    if (arrived >= nt) {
+      // the counter was not at a launch boundary when this launch began
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_or(a.norm_err, kNormErrWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
     if (arrived < nt - helpers) return;
     // Wait for the band's last arrival: agent-scope loads read the counter in
     // L2.  At most n_helpers - 1 workgroups of a band wait, and only once
     // their own tile is done; the launcher keeps their number over the
     // XCD's bands below its workgroup slots, so the bands' other workgroups
     // can always run.  The wait is bounded all the same; one that runs out
-    // sets bit 2 of norm_err.
+    // sets kNormErrWait.
     if (threadIdx.x == 0) {
       const unsigned long long target = v - arrived + nt;
       for (int it = 0; (long long)(__hip_atomic_load(cnt, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT) - target) < 0;
            ++it) {
         if (it == (1 << 18)) {
-          __hip_atomic_fetch_or(a.norm_err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_or(a.norm_err, kNormErrWait, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -1009,6 +1032,17 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     // L1 may hold lines of them from before the other workgroups' stores (an
     // L1 invalidate would do too, but buffer_inv sc1 also drops the XCD's
     // clean L2 lines, which the band's neighbours are still reading).
+    // The band's last arrival checks the tags (their loads issued here, the
+    // comparison after its rows, so the check adds no wait): every other tile
+    // counted itself before it, each after its tag was in L2, so every tag of
+    // this launch is in this XCD's L2 and names this XCD.  A tile that ran on
+    // another XCD left its tag, like its rows, in that XCD's L2 (here the
+    // consumed tag of the last launch is read), or names that XCD.  Then the
+    // tags are consumed.
+    const bool checker = arrived == nt - 1 && threadIdx.x < nt;
+    unsigned long long tag = 0;
+    if (checker) tag = __hip_atomic_load(cnt + 1 + threadIdx.x, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
     const int h = (int)(arrived - (nt - helpers));
     float* const xt = reinterpret_cast<float*>(&smem[0][0]) + wave * kRmsRowLds<4>;
     for (int rr = h + (int)helpers * wave; rr < BM; rr += (int)helpers * NW) {
@@ -1030,6 +1064,11 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
           norm_row_l2<4>(rs, a, r, lane, xt);
           break;
       }
+    }
+    if (checker) {
+      if (tag != (16ull | (unsigned long long)xcc))
+        __hip_atomic_fetch_or(a.norm_err, kNormErrXcd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(cnt + 1 + threadIdx.x, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -1138,26 +1177,50 @@ hipError_t launch_qkv_norm(const GemmArgs& a, hipStream_t st) {
 
 // The residual GEMM followed by the row norm of its result (kAccumNorm): the
 // residual tiles with all of a BM-row band on one XCD.
+// XCDs of the current device (hipDeviceAttributeNumberOfXccs), 0 if unknown;
+// cached per device.
+int device_xccs() {
+  constexpr int kDevs = 64;
+  static int cache[kDevs] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kDevs && cache[dev]) return cache[dev];
+  int x = 0;
+  if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x <= 0)
+    return 0;
+  if (dev < kDevs) cache[dev] = x;
+  return x;
+}
+
 // Helpers per band: as many as the waiting ones leave the bands' other
 // workgroups room.  A band's waiting workgroups (helpers - 1 at most) hold
 // their slots until the band completes; over the bands one XCD holds at once
 // (all of its bands, at worst) they must stay below the XCD's workgroup slots
-// (resident workgroups per CU x CUs per XCD, 32 on MI355X), so that every
-// band's remaining workgroups can still be dispatched.  Measured at M = 600
-// (LM step, 19 bands): 32 helpers (one row each) 2.307 ms, 16 2.311, 8 2.34,
-// 4 2.49: the more CUs share a band's rows, the shorter the launch's tail.
+// (resident workgroups per CU x CUs per XCD), so that every band's remaining
+// workgroups can still be dispatched.  CUs per XCD come from the device's CU
+// and XCD counts (32 on MI355X: 256 CUs in 8 XCDs).  Measured at M = 600 (LM
+// step, 19 bands, 32 column tiles): at most 16 helpers (two rows each, one
+// per wavefront) 2.223-2.225 ms against 2.229-2.238 for 32 and 2.232-2.234
+// for 8 (same box, alternating); 4 helpers (8 rows, two per wavefront) cost
+// 2.3 us more per launch.
 int norm_helpers(int occ, int64_t bands) {
   int dev = 0, cus = 0;
+  const int xcds = device_xccs();
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0 || occ <= 0)
+      cus <= 0 || occ <= 0 || xcds <= 0)
     return 1;
-  const int xcds = cus >= 64 ? cus / 32 : 1;
   const int64_t per_xcd = (bands + xcds - 1) / xcds, slots = (int64_t)occ * (cus / xcds);
   int h = kMaxNormHelpers;
   while (h > 1 && (int64_t)(h - 1) * per_xcd >= slots) h /= 2;
   return h;
 }
+
+}  // namespace
+
+bool norm_fusable() { return device_xccs() == kBandXcds; }
+
+namespace {
 
 template <int BN, int BM, int WN, int WM, int SB, int NST, bool PIPE>
 hipError_t launch_norm_cfg(const GemmArgs& a, int64_t slot0, hipStream_t st) {
@@ -1188,6 +1251,8 @@ hipError_t launch_gemm_norm(const GemmArgs& a, hipStream_t st) {
   if (a.Kb % 4 || a.nslices != 1 || !a.out[0] || !a.nw || !a.nq || !a.nsc || !a.band_cnt ||
       !a.norm_err || a.N % 256 || a.N < 256 || a.N > 1024 || a.W16 || a.aq16)
     return hipErrorInvalidValue;
+  // the band placement takes workgroup id % 8 for the XCD
+  if (!norm_fusable()) return hipErrorNotSupported;
   const int64_t M = a.M;
   if (M >= 2048) return launch_norm_cfg<128, 64, 4, 2, 4, 2, false>(a, kLargeMBandBase, st);
   if (M < 512 && a.Kb % 8 == 0) return launch_norm_cfg<32, 32, 2, 2, 8, 3, true>(a, 0, st);

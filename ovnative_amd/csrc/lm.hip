@@ -22,6 +22,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <numeric>
@@ -395,6 +397,28 @@ struct OvhLm {
   std::vector<float> tab_host;
   float* d_tab = nullptr;
   size_t tab_cap = 0;
+  // In-runner recovery: the fallbacks taken (OVH_LM_RECOVERED_*), a condition
+  // to force on the next forward (OVH_LM_FORCE_*), and the host inputs of the
+  // last forward that left its logits on the device without synchronising,
+  // so that the sample which finds its flags set can run it again.
+  int recovered = 0;
+  uint32_t last_flags = 0;  // the flag word of the last flagged forward
+  int force = 0;
+  struct LastForward {
+    bool valid = false;
+    int batch = 0, seq = 0;
+    std::vector<int64_t> ids, pos, seg_row0;
+    std::vector<uint8_t> am, masks;  // the segments' masks, concatenated
+    std::vector<int> seg_rows;
+    std::vector<int64_t> mask_off;   // offset of each segment's mask, -1: none
+  } last;
+  // Stage timer (ovh_lm_set_profile): events recorded between the stages of
+  // the last forward, their labels, and the per-label sums.
+  bool profile = false, profile_print = false;
+  std::vector<hipEvent_t> prof_ev;
+  std::vector<const char*> prof_lab;
+  size_t prof_n = 0;
+  std::vector<std::pair<const char*, double>> prof_ms;
 
   ~OvhLm() {
     for (auto& L : layers) {
@@ -415,6 +439,7 @@ struct OvhLm {
     if (d_overflow) (void)hipFree(d_overflow);
     if (d_band) (void)hipFree(d_band);
     if (graph) (void)hipGraphExecDestroy(graph);
+    for (hipEvent_t e : prof_ev) (void)hipEventDestroy(e);
     if (own_st) (void)hipStreamDestroy(own_st);
   }
 };
@@ -653,6 +678,33 @@ bool all_ones(const uint8_t* m, int64_t n) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// The stage timer's sums for the forward just enqueued: waits for its last
+// event, then adds each stage's time (from the mark before it) to its label,
+// labels in the order they first appear.
+int stage_times(OvhLm& L) {
+  L.prof_ms.clear();
+  if (L.prof_n < 2) return OV_OK;
+  OVH_HIP(hipEventSynchronize(L.prof_ev[L.prof_n - 1]), "stage timer: hipEventSynchronize");
+  for (size_t i = 1; i < L.prof_n; ++i) {
+    float ms = 0.f;
+    OVH_HIP(hipEventElapsedTime(&ms, L.prof_ev[i - 1], L.prof_ev[i]),
+            "stage timer: hipEventElapsedTime");
+    auto it = std::find_if(L.prof_ms.begin(), L.prof_ms.end(), [&](const auto& kv) {
+      return std::strcmp(kv.first, L.prof_lab[i]) == 0;
+    });
+    if (it == L.prof_ms.end())
+      L.prof_ms.emplace_back(L.prof_lab[i], (double)ms);
+    else
+      it->second += ms;
+  }
+  if (L.profile_print) {
+    std::fprintf(stderr, "[hip-stage]");
+    for (const auto& kv : L.prof_ms) std::fprintf(stderr, " %s=%.3f", kv.first, kv.second);
+    std::fprintf(stderr, "\n");
+  }
+  return OV_OK;
+}
+
 // Forward over T rows laid out as `batch` x `seq` for the embedding's id indexing
 // ([batch, C, seq]), attention split into `segs`.
 int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
@@ -661,7 +713,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   const int64_t T = (int64_t)batch * seq;
   const int64_t H = c.hidden, D = c.head_dim, QD = (int64_t)c.n_heads * D,
                 KVD = (int64_t)c.n_kv_heads * D, I = c.inter, C = c.n_codebooks,
-                CV = (int64_t)c.n_codebooks * c.audio_vocab, half = D / 2;
+                CV = (int64_t)c.n_codebooks * c.audio_vocab;
   // Id range checks (Emb::gather throws on these, mat.cpp:58-60).
   for (int64_t b = 0; b < batch; ++b)
     for (int64_t s = 0; s < seq; ++s) {
@@ -702,7 +754,11 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   // the residual GEMMs' fused norm: tile-major codes, the int8 GEMM form,
   // below 2048 rows (from there, on 64-row bands, it measured no faster than
   // the separate norm: config 5 forward 39.5 against 39.4 ms)
-  const bool nfuse = L.norm_fused && tiled && !f16 && T < 2048;
+  const bool nfuse = L.norm_fused && tiled && !f16 && T < 2048 && ovh::norm_fusable();
+  // a condition forced from the host (ovh_lm_force_condition) for this forward
+  const int force = L.force;
+  L.force = 0;
+  const int xcd_test = (force & OVH_LM_FORCE_XCD) ? 1 : 0;
   // L2 prefetch of o_proj's weight by the attention launch (below 2048 rows,
   // int8 form).  With the fused norm every XCD reads the whole weight (its own
   // row bands), so every XCD loads all of it; the plain residual launch's XCDs
@@ -731,6 +787,14 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
             "hipMalloc(band counters)");
     OVH_HIP(hipMemset(L.d_band, 0, sizeof(unsigned long long) * words), "hipMemset(band counters)");
     L.band_words = words;
+  }
+  if (nfuse && (force & OVH_LM_FORCE_BAND_WAIT)) {
+    // the first band's counter one short of a launch boundary: its first
+    // arrival finds the counter off the boundary, the others wait for an
+    // arrival that never comes until their bounded wait runs out
+    OVH_HIP(hipStreamSynchronize(L.st), "hipStreamSynchronize");
+    const unsigned long long off = ovh::kBandRound - 1;
+    OVH_HIP(hipMemcpy(L.d_band, &off, sizeof off, hipMemcpyHostToDevice), "force band counter");
   }
   std::vector<int64_t> bias_off(segs.size(), -1), bits_off(segs.size(), -1);
   int64_t bias_elems = 0, bits_words = 0;
@@ -910,6 +974,21 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     sp.asc = asc;
     sp.aq_tiled = tiled;
   }
+  // stage timer: an event after each stage, labelled with the stage
+  L.prof_n = 0;
+  auto mark = [&](const char* label) -> int {
+    if (!L.profile) return OV_OK;
+    if (L.prof_n == L.prof_ev.size()) {
+      hipEvent_t e = nullptr;
+      OVH_HIP(hipEventCreate(&e), "hipEventCreate(stage timer)");
+      L.prof_ev.push_back(e);
+      L.prof_lab.push_back(nullptr);
+    }
+    L.prof_lab[L.prof_n] = label;
+    OVH_HIP(hipEventRecord(L.prof_ev[L.prof_n++], st), "hipEventRecord(stage timer)");
+    return OV_OK;
+  };
+  if ((rc = mark("start")) != OV_OK) return rc;
   // The inputs go up first, in one copy; the staging buffer may be refilled
   // once it is done.
   OVH_HIP(hipMemcpyAsync(d_in, L.h_in, in_bytes, hipMemcpyHostToDevice, st), "upload inputs");
@@ -946,6 +1025,7 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
     hipLaunchKernelGGL(ovh::embed_kernel, dim3((unsigned)(T + mask_wgs)), dim3(256), 0, st, d_ids,
                        d_am, seq, (int)C, H, L.tok, L.aud, L.d_offsets, x, T, mj, en);
     OVH_HIP(hipGetLastError(), "embed launch");
+    if ((rc = mark("prep+embed")) != OV_OK) return rc;
     const int64_t qkv_n[3] = {QD, KVD, KVD};
     float* qkv_c[3] = {q, k, v};
     const int64_t gu_n[2] = {I, I};
@@ -977,37 +1057,43 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           ga.aq16 = aq16;
         }
         OVH_HIP(ovh::launch_gemm(ga, ovh::kQkvNorm, st), "q/k/v + qk-norm launch");
+        if ((rc = mark("qkv")) != OV_OK) return rc;
         sp.pf = prefetch_of(Y.o, kPfAttnWgs);
         OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
         sp.pf = ovh::L2Prefetch{};
       } else if ((rc = ovh::linear_q_sliced(T, aq, asc, Y.qkv, qkv_n, qkv_c, 3, st, tiled, aq16,
-                                            f16)) != OV_OK) {
+                                            f16)) != OV_OK || (rc = mark("qkv")) != OV_OK) {
         return rc;
       } else if (split) {
         // q/k norm + RoPE, f16 planes of k and V, then attention
         OVH_HIP(ovh::launch_qk_norm_rope_split(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, cosb,
                                                sinb, c.rms_eps, aargs, sp, max_rows, st),
                 "qk_norm_rope launch");
+        if ((rc = mark("qk_norm_rope")) != OV_OK) return rc;
         OVH_HIP(ovh::launch_attention_split_only(aargs, sp, max_rows, true, st), "attention launch");
       } else {
         if ((rc = ovh_qk_norm_rope(q, k, Y.qn, Y.kn, T, c.n_heads, c.n_kv_heads, (int)D, cosb,
-                                   sinb, c.rms_eps, st)) != OV_OK)
+                                   sinb, c.rms_eps, st)) != OV_OK ||
+            (rc = mark("qk_norm_rope")) != OV_OK)
           return rc;
         if ((rc = ovh_attention(asegs.data(), (int)asegs.size(), c.n_heads, c.n_kv_heads, (int)D, q,
                                 QD, k, v, KVD, scale, att, QD, st)) != OV_OK)
           return rc;
       }
       if (!split && (rc = ovh_s8_nk_quantize(T, QD, att, aq, asc, st)) != OV_OK) return rc;
+      if ((rc = mark("attn")) != OV_OK) return rc;
       // x += o_proj(attention), then the post-attention norm's codes: in one
       // launch into aq2/asc2, or a second launch into aq/asc
       const int8_t* naq = nfuse ? aq2 : aq;
       const float* nasc = nfuse ? asc2 : asc;
       if (nfuse) {
         if ((rc = ovh::linear_q_norm(T, aq, asc, Y.o, x, H, Y.ln2, c.rms_eps, aq2, asc2, L.d_band,
-                                     L.d_overflow, st)) != OV_OK)
+                                     L.d_overflow, st, xcd_test)) != OV_OK ||
+            (rc = mark("o_proj")) != OV_OK)
           return rc;
       } else {
         if ((rc = ovh::linear_q(T, aq, asc, Y.o, x, H, 1, st, tiled, aq16, f16)) != OV_OK) return rc;
+        if ((rc = mark("o_proj")) != OV_OK) return rc;
         if ((rc = norm_q(Y.ln2)) != OV_OK) return rc;
       }
       // the norm after down: the next layer's input norm, or the final norm of
@@ -1037,9 +1123,10 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
           ga.aq16 = aq16;
         }
         OVH_HIP(ovh::launch_gemm(ga, ovh::kSiluQuant, st), "gate/up + silu launch");
+        if ((rc = mark("gate_up")) != OV_OK) return rc;
         if (nfuse && next_ln) {
           if ((rc = ovh::linear_q_norm(T, ga.hq, ga.hsc, Y.down, x, H, next_ln, c.rms_eps, aq, asc,
-                                       L.d_band, L.d_overflow, st)) != OV_OK)
+                                       L.d_band, L.d_overflow, st, xcd_test)) != OV_OK)
             return rc;
         } else if ((rc = ovh::linear_q(T, ga.hq, ga.hsc, Y.down, x, H, 1, st, tiled, aq16, f16)) !=
                    OV_OK) {
@@ -1047,9 +1134,12 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
         }
       } else {
         if ((rc = ovh_linear_q_sliced(T, aq, asc, Y.gate_up, gu_n, gu_c, 2, st)) != OV_OK) return rc;
+        if ((rc = mark("gate_up")) != OV_OK) return rc;
         if ((rc = ovh_silu_mul_quantize(T, I, gate, up, aq, asc, st)) != OV_OK) return rc;
+        if ((rc = mark("silu")) != OV_OK) return rc;
         if ((rc = ovh_linear_q(T, aq, asc, Y.down, x, H, 1, st)) != OV_OK) return rc;
       }
+      if ((rc = mark("down")) != OV_OK) return rc;
     }
     if (head_f32) {
       // rmsnorm_f32 then Mat's fp32 product (lm.cpp:383-385)
@@ -1072,20 +1162,23 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
                                         static_cast<float*>(at(b_hs)), st),
               "final norm (split) launch");
       OVH_HIP(ovh::launch_gemm_f32(ha, st), "fp32 head launch");
-      return OV_OK;
+      return mark("final_norm+head");
     }
     if (!nfuse && (rc = norm_q(L.final_norm)) != OV_OK) return rc;
-    return ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled, aq16, f16);
+    if ((rc = ovh::linear_q(T, aq, asc, L.head, logits, CV, 0, st, tiled, aq16, f16)) != OV_OK)
+      return rc;
+    return mark("final_norm+head");
   };
 
-  if (!L.use_graphs) {
+  if (!L.use_graphs || L.profile) {
     if ((rc = enqueue()) != OV_OK) return rc;
+    if (L.profile && (rc = stage_times(L)) != OV_OK) return rc;
   } else {
     // One graph per forward layout: the shapes, the segments and their masks,
     // and every buffer address the launches take.  A changed layout (other
     // lengths, a grown arena, new RoPE tables) is captured anew; the same
     // layout replays over the new inputs the upload above brought.
-    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, f16, nfuse, pf_on,
+    std::vector<int64_t> key = {batch, seq, split, L.silu_fused, f16, nfuse, pf_on, xcd_test,
                                 (int64_t)(intptr_t)L.d_band, (int64_t)segs.size(),
                                 (int64_t)in_bytes, (int64_t)(intptr_t)L.arena,
                                 (int64_t)(intptr_t)cosb, (int64_t)(intptr_t)sinb};
@@ -1120,20 +1213,95 @@ int forward_rows(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs,
   return OV_OK;
 }
 
-// The split attention reports |k| or |v| beyond the f16 range through a device
-// flag; checked (and cleared) wherever the runner synchronises with the host.
-int check_overflow(OvhLm& L) {
-  uint32_t flag = 0;
-  OVH_HIP(hipMemcpy(&flag, L.d_overflow, sizeof flag, hipMemcpyDeviceToHost), "read overflow flag");
-  if (!flag) return OV_OK;
-  const uint32_t zero = 0;
-  OVH_HIP(hipMemcpy(L.d_overflow, &zero, sizeof zero, hipMemcpyHostToDevice), "clear overflow flag");
-  if (flag & 2u)
-    return set_error(OV_ERR_INTERNAL, "residual GEMM + norm: a band hand-off wait ran out (the "
-                                      "band's workgroups did not all run): switch to "
-                                      "ovh_lm_set_fused_norm(lm, 0)");
-  return set_error(OV_ERR_INTERNAL, "attention inputs beyond the f16 range for the split-f16 "
-                                    "kernel: switch to ovh_lm_set_attention(lm, 0)");
+// The runner's flag word (d_overflow): kFlagAttn, |k| or |v| beyond the f16
+// range of the split attention (set by the q/k/v epilogue or the plane
+// split); ovh::kNormErrWait / kNormErrXcd, a fused residual + norm launch's
+// band hand-off failed.  Read, and cleared, where the runner synchronises
+// with the host.
+constexpr uint32_t kFlagAttn = 1u;
+constexpr uint32_t kFlagNorm = ovh::kNormErrWait | ovh::kNormErrXcd;
+
+int take_flags(OvhLm& L, uint32_t* flag) {
+  *flag = 0;
+  OVH_HIP(hipMemcpy(flag, L.d_overflow, sizeof *flag, hipMemcpyDeviceToHost), "read runner flags");
+  if (*flag) {
+    L.last_flags = *flag;
+    const uint32_t zero = 0;
+    OVH_HIP(hipMemcpy(L.d_overflow, &zero, sizeof zero, hipMemcpyHostToDevice),
+            "clear runner flags");
+  }
+  return OV_OK;
+}
+
+int flag_error(uint32_t flag) {
+  if (flag & kFlagNorm)
+    return set_error(OV_ERR_INTERNAL, "residual GEMM + norm: the row bands' hand-off failed "
+                                      "again with the norm as a launch of its own");
+  return set_error(OV_ERR_INTERNAL, "attention inputs beyond the f16 range with the fp32 "
+                                    "attention form selected");
+}
+
+// Switch to the exact fallbacks the flag calls for and keep them; false when
+// a flagged condition has no fallback left (its form is already off).
+int fall_back(OvhLm& L, uint32_t flag, bool* ok) {
+  *ok = true;
+  if (flag & kFlagAttn) {
+    if (!L.attn_split) *ok = false;
+    L.attn_split = false;
+    L.recovered |= OVH_LM_RECOVERED_ATTENTION;
+  }
+  if (flag & kFlagNorm) {
+    if (!L.norm_fused) *ok = false;
+    L.norm_fused = false;
+    L.recovered |= OVH_LM_RECOVERED_NORM;
+    // the counters may stand anywhere now: from zero if the fused norm is
+    // switched on again
+    if (L.d_band) {
+      OVH_HIP(hipStreamSynchronize(L.st), "hipStreamSynchronize");
+      OVH_HIP(hipMemset(L.d_band, 0, sizeof(unsigned long long) * (size_t)L.band_words),
+              "reset band counters");
+    }
+  }
+  return OV_OK;
+}
+
+// The forward the runner may have to run again: its host inputs, kept when it
+// left the logits on the device without synchronising.
+int keep_last(OvhLm& L, int batch, int seq, const std::vector<SegIn>& segs, const int64_t* ids,
+              const uint8_t* audio_mask, const int64_t* pos) {
+  OvhLm::LastForward& f = L.last;
+  const int64_t T = (int64_t)batch * seq;
+  f.valid = false;
+  f.batch = batch;
+  f.seq = seq;
+  f.ids.assign(ids, ids + T * L.cfg.n_codebooks);
+  f.am.assign(audio_mask, audio_mask + T);
+  f.pos.assign(pos, pos + T);
+  f.seg_rows.clear();
+  f.seg_row0.clear();
+  f.mask_off.clear();
+  f.masks.clear();
+  for (const SegIn& g : segs) {
+    f.seg_rows.push_back(g.rows);
+    f.seg_row0.push_back(g.row0);
+    if (g.mask) {
+      f.mask_off.push_back((int64_t)f.masks.size());
+      f.masks.insert(f.masks.end(), g.mask, g.mask + (size_t)g.rows * (size_t)g.rows);
+    } else {
+      f.mask_off.push_back(-1);
+    }
+  }
+  f.valid = true;
+  return OV_OK;
+}
+
+int run_last(OvhLm& L) {
+  const OvhLm::LastForward& f = L.last;
+  std::vector<SegIn> segs(f.seg_rows.size());
+  for (size_t i = 0; i < segs.size(); ++i)
+    segs[i] = SegIn{f.mask_off[i] < 0 ? nullptr : f.masks.data() + f.mask_off[i], f.seg_rows[i],
+                    f.seg_row0[i]};
+  return forward_rows(L, f.batch, f.seq, segs, f.ids.data(), f.am.data(), f.pos.data());
 }
 
 bool config_ok(const OvhLmConfig& c) {
@@ -1177,6 +1345,8 @@ int ovh_lm_create(const OvhLmConfig* cfg, const OvhTensorView* tensors, int n_te
   // the SiLU-fused gate/up GEMM takes K = hidden in 4-block stages (hidden a
   // multiple of 128); other widths compose the sliced GEMM and silu_mul_quantize
   L->silu_fused = cfg->inter % 64 == 0 && cfg->hidden % 128 == 0;
+  // the stage timer from the environment, printing as the reference's does
+  if (std::getenv("OVH_LM_PROFILE")) L->profile = L->profile_print = true;
   int rc = OV_OK;
   if (hipMalloc(reinterpret_cast<void**>(&L->d_overflow), sizeof(uint32_t)) != hipSuccess ||
       hipMemset(L->d_overflow, 0, sizeof(uint32_t)) != hipSuccess)
@@ -1209,16 +1379,29 @@ int ovh_lm_forward(OvhLm* lm, int batch, int seq, const int64_t* input_ids,
     segs[(size_t)b] = SegIn{attn_mask + (int64_t)b * seq * seq, seq, (int64_t)b * seq};
   int rc = forward_rows(*lm, batch, seq, segs, input_ids, audio_mask, position_ids);
   if (rc != OV_OK) return rc;
-  if (!logits || lm->device_sampling) return OV_OK;
+  // logits left on the device: the sample that reads them checks the flags
+  if (!logits || lm->device_sampling)
+    return keep_last(*lm, batch, seq, segs, input_ids, audio_mask, position_ids);
+  lm->last.valid = false;
   // [B*S, C*V] on the device -> [B, C, S, V] on the host (cuda_lm.cu:1184-1199).
   const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab;
   const size_t n = (size_t)batch * seq * C * V;
   lm->host_flat.resize(n);
-  OVH_HIP(hipMemcpyAsync(lm->host_flat.data(), lm->logits, sizeof(float) * n,
-                         hipMemcpyDeviceToHost, lm->st),
-          "download logits");
-  OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
-  if ((rc = check_overflow(*lm)) != OV_OK) return rc;
+  for (;;) {
+    OVH_HIP(hipMemcpyAsync(lm->host_flat.data(), lm->logits, sizeof(float) * n,
+                           hipMemcpyDeviceToHost, lm->st),
+            "download logits");
+    OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
+    uint32_t flag = 0;
+    bool ok = true;
+    if ((rc = take_flags(*lm, &flag)) != OV_OK) return rc;
+    if (!flag) break;
+    // the forward again on the fallback its flags call for
+    if ((rc = fall_back(*lm, flag, &ok)) != OV_OK) return rc;
+    if (!ok) return flag_error(flag);
+    if ((rc = forward_rows(*lm, batch, seq, segs, input_ids, audio_mask, position_ids)) != OV_OK)
+      return rc;
+  }
   for (int b = 0; b < batch; ++b)
     for (int cb = 0; cb < C; ++cb)
       for (int s = 0; s < seq; ++s)
@@ -1240,12 +1423,23 @@ int ovh_lm_forward_cfg(OvhLm* lm, int cond_seq, int uncond_seq, const int64_t* i
   std::vector<SegIn> segs = {SegIn{cond_attn, cond_seq, 0}, SegIn{uncond_attn, uncond_seq, cond_seq}};
   int rc = forward_rows(*lm, 1, rows, segs, input_ids, audio_mask, position_ids);
   if (rc != OV_OK) return rc;
-  if (!logits || lm->device_sampling) return OV_OK;
+  if (!logits || lm->device_sampling)
+    return keep_last(*lm, 1, rows, segs, input_ids, audio_mask, position_ids);
+  lm->last.valid = false;
   const size_t n = (size_t)rows * lm->cfg.n_codebooks * lm->cfg.audio_vocab;
-  OVH_HIP(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n, hipMemcpyDeviceToHost, lm->st),
-          "download logits");
-  OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
-  return check_overflow(*lm);
+  for (;;) {
+    OVH_HIP(hipMemcpyAsync(logits, lm->logits, sizeof(float) * n, hipMemcpyDeviceToHost, lm->st),
+            "download logits");
+    OVH_HIP(hipStreamSynchronize(lm->st), "forward sync");
+    uint32_t flag = 0;
+    bool ok = true;
+    if ((rc = take_flags(*lm, &flag)) != OV_OK) return rc;
+    if (!flag) return OV_OK;
+    if ((rc = fall_back(*lm, flag, &ok)) != OV_OK) return rc;
+    if (!ok) return flag_error(flag);
+    if ((rc = forward_rows(*lm, 1, rows, segs, input_ids, audio_mask, position_ids)) != OV_OK)
+      return rc;
+  }
 }
 
 const void* ovh_lm_last_logits(const OvhLm* lm) { return lm ? lm->logits : nullptr; }
@@ -1270,6 +1464,30 @@ void ovh_lm_set_prefetch(OvhLm* lm, int on) {
   if (lm) lm->prefetch = on != 0;
 }
 
+int ovh_lm_recovered(const OvhLm* lm) { return lm ? lm->recovered : 0; }
+
+int ovh_lm_last_flags(const OvhLm* lm) { return lm ? (int)lm->last_flags : 0; }
+
+void ovh_lm_force_condition(OvhLm* lm, int what) {
+  if (lm) lm->force = what & (OVH_LM_FORCE_BAND_WAIT | OVH_LM_FORCE_XCD);
+}
+
+void ovh_lm_set_profile(OvhLm* lm, int on) {
+  if (!lm) return;
+  lm->profile = on != 0;
+  if (!on) lm->profile_print = false;
+}
+
+int ovh_lm_stage_times(const OvhLm* lm, double* ms, const char** names, int n) {
+  if (!lm) return 0;
+  const int k = (int)lm->prof_ms.size();
+  for (int i = 0; i < k && i < n; ++i) {
+    if (ms) ms[i] = lm->prof_ms[(size_t)i].second;
+    if (names) names[i] = lm->prof_ms[(size_t)i].first;
+  }
+  return k;
+}
+
 int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond, int uncond_seq,
                   int target_len, float guidance, float layer_penalty, int32_t* pred,
                   float* scores) {
@@ -1279,7 +1497,7 @@ int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond,
     return set_error(OV_ERR_INVALID_ARG, "sample: need 0 < target_len <= both plane lengths");
   const int C = lm->cfg.n_codebooks, V = lm->cfg.audio_vocab;
   const int64_t n = (int64_t)C * target_len;
-  constexpr size_t kHead = 64;  // overflow flag, padded
+  constexpr size_t kHead = 64;  // the runner's flag word, padded
   if (n > lm->sample_cap) {
     OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
     if (lm->d_out) OVH_HIP(hipFree(lm->d_out), "hipFree");
@@ -1296,22 +1514,52 @@ int ovh_lm_sample(OvhLm* lm, const void* cond, int cond_seq, const void* uncond,
   const size_t bytes = kHead + 8 * (size_t)n;
   int32_t* d_pred = reinterpret_cast<int32_t*>(lm->d_out + kHead);
   float* d_scores = reinterpret_cast<float*>(lm->d_out + kHead + 4 * (size_t)n);
-  // The mask token is the last audio id (kMaskId = 1024 with audio_vocab 1025,
-  // cpp/src/model/tts.cpp:17).
-  hipLaunchKernelGGL(ovh::guided_sample_kernel, dim3((unsigned)n), dim3(ovh::kSampleThreads), 0,
-                     lm->st, static_cast<const float*>(cond), cond_seq,
-                     static_cast<const float*>(uncond), C, V, target_len, guidance, layer_penalty,
-                     V - 1, d_pred, d_scores, lm->d_overflow,
-                     reinterpret_cast<uint32_t*>(lm->d_out));
-  OVH_HIP(hipGetLastError(), "guided sample launch");
-  OVH_HIP(hipMemcpyAsync(lm->h_out, lm->d_out, bytes, hipMemcpyDeviceToHost, lm->st),
-          "download sample");
-  OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
+  for (;;) {
+    // The mask token is the last audio id (kMaskId = 1024 with audio_vocab
+    // 1025, cpp/src/model/tts.cpp:17).
+    hipLaunchKernelGGL(ovh::guided_sample_kernel, dim3((unsigned)n), dim3(ovh::kSampleThreads), 0,
+                       lm->st, static_cast<const float*>(cond), cond_seq,
+                       static_cast<const float*>(uncond), C, V, target_len, guidance,
+                       layer_penalty, V - 1, d_pred, d_scores, lm->d_overflow,
+                       reinterpret_cast<uint32_t*>(lm->d_out));
+    OVH_HIP(hipGetLastError(), "guided sample launch");
+    OVH_HIP(hipMemcpyAsync(lm->h_out, lm->d_out, bytes, hipMemcpyDeviceToHost, lm->st),
+            "download sample");
+    OVH_HIP(hipStreamSynchronize(lm->st), "sample sync");
+    uint32_t flag;
+    std::memcpy(&flag, lm->h_out, sizeof flag);
+    if (!flag) break;
+    int rc = take_flags(*lm, &flag);
+    if (rc != OV_OK) return rc;
+    // Planes of the last forward (logits left on the device): that forward
+    // again on its fallback, then this sample on its new logits (the arena
+    // may have moved: same offsets).
+    const char* base = reinterpret_cast<const char*>(lm->logits);
+    // the last forward's logits: [rows][C * V], ids [C * rows]
+    const size_t plane_bytes = lm->last.valid ? sizeof(float) * lm->last.ids.size() * (size_t)V : 0;
+    auto own = [&](const void* p) {
+      const char* c = static_cast<const char*>(p);
+      return base && c >= base && c < base + plane_bytes;
+    };
+    if (!lm->last.valid || !own(cond) || !own(uncond))
+      return set_error(OV_ERR_INTERNAL,
+                       (flag & kFlagNorm)
+                           ? "the last forward's residual GEMM + norm hand-off failed: its "
+                             "logits are not to be used (ovh_lm_set_fused_norm(lm, 0))"
+                           : "the last forward's attention inputs were beyond the f16 range: its "
+                             "logits are not to be used (ovh_lm_set_attention(lm, 0))");
+    const ptrdiff_t oc = static_cast<const char*>(cond) - base,
+                    ou = static_cast<const char*>(uncond) - base;
+    bool ok = true;
+    if ((rc = fall_back(*lm, flag, &ok)) != OV_OK) return rc;
+    if (!ok) return flag_error(flag);
+    if ((rc = run_last(*lm)) != OV_OK) return rc;
+    cond = reinterpret_cast<const char*>(lm->logits) + oc;
+    uncond = reinterpret_cast<const char*>(lm->logits) + ou;
+  }
   std::memcpy(pred, lm->h_out + kHead, 4 * (size_t)n);
   std::memcpy(scores, lm->h_out + kHead + 4 * (size_t)n, 4 * (size_t)n);
-  uint32_t flag;
-  std::memcpy(&flag, lm->h_out, sizeof flag);
-  return flag ? check_overflow(*lm) : OV_OK;
+  return OV_OK;
 }
 
 

@@ -105,17 +105,14 @@ __device__ __forceinline__ float quant_block_lane(const float v[4], int nvalid, 
 // 0..7 stream their chains with ds_read_b128; the 8 chains are added in order.
 template <int P>
 constexpr int kRmsRowLds = 8 * (32 * P + 4);
-// rms_quant_row_vals takes the row's values already loaded (xv[p] = elements
-// 256p + 4l..+3).
+// rms_quant_row_wvals takes the row's values and its lane's norm weights
+// already loaded (xv[p], wv[p] = elements 256p + 4l..+3).
 template <int P>
-__device__ __forceinline__ void rms_quant_row_vals(const f32x4 (&xv)[P], const float* __restrict__ w,
-                                                   float eps, int8_t* __restrict__ aq,
-                                                   float* __restrict__ asc, int64_t r, bool tiled,
-                                                   int lane, float* xt) {
+__device__ __forceinline__ void rms_quant_row_wvals(const f32x4 (&xv)[P], const f32x4 (&wv)[P],
+                                                    float eps, int8_t* __restrict__ aq,
+                                                    float* __restrict__ asc, int64_t r, bool tiled,
+                                                    int lane, float* xt) {
   constexpr int cols = 256 * P, T = cols / 8, TP = T + 4;  // chain length, padded LDS row
-  f32x4 wv[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
   // element 256p + 4l + c -> chain 4(l&1) + c, position 32p + l/2
 #pragma unroll
   for (int p = 0; p < P; ++p)
@@ -151,6 +148,17 @@ __device__ __forceinline__ void rms_quant_row_vals(const f32x4 (&xv)[P], const f
     *reinterpret_cast<uint32_t*>(aq + act_index(r, 256 * p + 4 * lane, cols, tiled)) = codes;
     if ((lane & 7) == 0) asc[r * (cols / 32) + 8 * p + (lane >> 3)] = s;
   }
+}
+
+template <int P>
+__device__ __forceinline__ void rms_quant_row_vals(const f32x4 (&xv)[P], const float* __restrict__ w,
+                                                   float eps, int8_t* __restrict__ aq,
+                                                   float* __restrict__ asc, int64_t r, bool tiled,
+                                                   int lane, float* xt) {
+  f32x4 wv[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) wv[p] = *reinterpret_cast<const f32x4*>(w + 256 * p + 4 * lane);
+  rms_quant_row_wvals<P>(xv, wv, eps, aq, asc, r, tiled, lane, xt);
 }
 
 template <int P>

@@ -39,12 +39,12 @@ int linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const OvhWeig
 // rmsnorm_quantize of the updated rows with weight nw into codes nq
 // (tile-major) and scales nsc, in the same launch (GemmMode kAccumNorm:
 // N = 256 P with P <= 4, K a multiple of 128).  band_cnt: the launch's band
-// counters (band_counter_words(M) or more, zero when allocated, kept
-// for every later launch with the same N); err gets bit 2 if a hand-off wait
-// ran out.
+// counters (band_counter_words(M) or more, zero when allocated, kept for
+// every later launch); err gets kNormErrWait / kNormErrXcd (gemm.h) when the
+// band hand-off failed.  xcd_test: GemmArgs::xcd_test (0 in use).
 int linear_q_norm(int64_t M, const int8_t* aq, const float* asc, const OvhWeight* w, float* x,
                   int64_t ldx, const float* nw, float eps, int8_t* nq, float* nsc,
-                  unsigned long long* band_cnt, uint32_t* err, hipStream_t st);
+                  unsigned long long* band_cnt, uint32_t* err, hipStream_t st, int xcd_test = 0);
 // The int8-valued f16 copy of w's tiles (DeviceWeight::q16) for the large-M
 // GEMM form, made on first call (hipMalloc, widened on st, then st synchronised;
 // serialised over threads).  False where it cannot be made now: during graph

@@ -94,3 +94,26 @@ def make_inputs(seed: int, cfg: dict, batch: int, seq: int, text: int):
         amask[1, :T] = 1
     pos = np.tile(np.arange(seq, dtype=np.int64), (batch, 1))
     return ids, amask, attn, pos
+
+
+# A hand-worked case of the guided sampling pass (tts.cpp:296-326, the device
+# form of cuda_lm.cu:679-758): V = 4 (token 3 is the mask token), 2 codebooks,
+# one frame, guidance g = 2, layer penalty 5.  With lc = log_softmax(cond) and
+# lu = log_softmax(uncond), mix = lc + g (lc - lu) = 3 cond - 2 uncond - K (K
+# a constant per row), then lp2 = log_softmax(mix), argmax over the non-mask
+# tokens, score = max lp2 - c * penalty:
+#   codebook 0: cond [0, 2, 1.5, 0], uncond [0, 3, 0.5, 0]: 3c - 2u = [0, 0, 3.5, 0]
+#     -> token 2, score 3.5 - ln(3 + e^3.5) = -0.0867208058559692;
+#   codebook 1: cond [1, 0, 0, 5], uncond [0, 0, 1, 5]: 3c - 2u = [3, 0, -2, 5]
+#     -> token 0 (the mask token's 5 is excluded), score
+#     3 - ln(e^3 + 1 + e^-2 + e^5) - 5 = -7.1336433595320905.
+# Plausible mistakes move the answer: the guidance term's sign flipped
+# (-lc + 2 lu: [0, 4, -0.5, 0] and [-1, 0, 2, 5]) picks tokens 1 and 2; no
+# guidance picks token 1 in codebook 0; the mask token not excluded picks 3 in
+# codebook 1; without the second log-softmax the scores are 1.9445 and
+# -7.0313; the penalty on codebook 0 instead of 1 moves both scores by 5.
+SAMPLER_CASE = dict(
+    cond=[[0.0, 2.0, 1.5, 0.0, 1.0, 0.0, 0.0, 5.0]],      # [frames, C * V], codebook-major
+    uncond=[[0.0, 3.0, 0.5, 0.0, 0.0, 0.0, 1.0, 5.0]],
+    C=2, V=4, T=1, guidance=2.0, penalty=5.0,
+    pred=[[2], [0]], scores=[[-0.0867208058559692], [-7.1336433595320905]])

@@ -703,3 +703,247 @@ def test_device_sampling_invariants(small_lm):
     assert np.array_equal(np_, bp)
     np.testing.assert_allclose(ns - 5.0 * np.arange(Cb)[:, None], bs, rtol=0, atol=8e-6)
     assert np.all(bp != V - 1) and np.all(p0 != V - 1)
+
+
+# ---------------------------------------------------------------------------
+# In-runner recovery (cuda_lm.cu:586-606, :620-622: the CUDA runner falls back
+# inside its forward when the fused attention cannot run).  The runner's
+# default kernels have two data- or machine-dependent failure conditions; each
+# is flagged on the device and the runner runs that forward again on the
+# exact fallback, keeps it, and returns the fallback's bits.
+
+def _lm(ts, cfg):
+    import ovnative_amd as ov
+    return ov.LM.from_tensors(ts, _cfg(cfg))
+
+
+def _overflowing_k(seed):
+    """SMALL with layer 1's k-norm weights x 1e5: the normalised keys reach
+    ~1e5, beyond f16, so the split-f16 attention cannot take them (the fp32
+    form can: scores stay far below the fp32 range)."""
+    from ovnative_amd import ovw1
+    ts, table = make_lm(seed, SMALL)
+    out = []
+    for t in ts:
+        if t.name == "llm.layers.1.self_attn.k_norm.weight":
+            t = ovw1.Tensor(t.name, (t.array * np.float32(1e5)).astype(np.float32))
+        out.append(t)
+    return out
+
+
+def test_normal_forward_takes_no_fallback(small_lm):
+    """On MI355X the default forms run without a flag: the fused norm's XCD
+    placement check (workgroup id % 8 = XCC_ID) holds and no fallback is taken."""
+    ts, table, lm = small_lm
+    x = make_inputs(201, SMALL, 2, 300, 12)
+    for _ in range(3):
+        lm.forward(*x)
+    assert lm.recovered() == 0
+
+
+def test_recovery_attention_overflow():
+    """Keys beyond the f16 range: the first forward flags the split-f16
+    attention, the runner runs it again on the fp32 form and returns exactly
+    the logits of a runner set to the fp32 form from the start; it stays there.
+    The same through device sampling (the sample finds the flag and runs the
+    forward again) and through ovh_lm_generate."""
+    import ovnative_amd as ov
+    ts = _overflowing_k(211)
+    x = make_inputs(212, SMALL, 2, 96, 12)
+    ref = _lm(ts, SMALL)
+    ref.set_attention(False)
+    want = ref.forward(*x)
+    assert np.isfinite(want).all()
+    lm = _lm(ts, SMALL)
+    try:
+        got = lm.forward(*x)
+        assert lm.recovered() == ov.RECOVERED_ATTENTION
+        assert np.array_equal(got.view(np.int32), want.view(np.int32))
+        got = lm.forward(*x)
+        assert np.array_equal(got.view(np.int32), want.view(np.int32))
+    finally:
+        lm.close()
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    S, T = 96, 84
+    plane = S * Cb * V * 4
+
+    def sample(runner):
+        runner.set_device_sampling(True)
+        try:
+            runner.forward(*x, host_logits=False)
+            base = runner.last_logits_ptr()
+            return runner.sample(base, S, base + plane, S, T, 2.0, 5.0)
+        finally:
+            runner.set_device_sampling(False)
+
+    want_p, want_s = sample(ref)
+    lm = _lm(ts, SMALL)
+    try:
+        p, s = sample(lm)
+        assert lm.recovered() == ov.RECOVERED_ATTENTION
+        assert np.array_equal(p, want_p) and np.array_equal(s.view(np.int32), want_s.view(np.int32))
+    finally:
+        lm.close()
+    prompt = x[0][0].copy()
+    prompt[:, S - T:] = V - 1
+    am = x[1][0]
+    opts = ov.GenOptions(num_steps=4)
+    want_t = ref.generate(prompt, am, T, opts)
+    lm = _lm(ts, SMALL)
+    try:
+        got_t = lm.generate(prompt, am, T, opts)
+        assert lm.recovered() == ov.RECOVERED_ATTENTION
+        assert np.array_equal(got_t, want_t)
+    finally:
+        lm.close()
+        ref.close()
+
+
+@pytest.mark.parametrize("what", ["band_wait", "xcd"])
+def test_recovery_fused_norm(what):
+    """A failed row-band hand-off in the fused residual + norm launch, forced
+    from the host (band_wait: the first band's counter one short of a launch
+    boundary, so the hand-off reports it and that band's helpers' bounded
+    waits run out; xcd: every workgroup's XCD placement check made to fail):
+    the runner runs the forward again with the norm as a launch of its own and
+    returns that setting's bits, also when the flag is found by the sample of
+    a device-sampling step, and in ovh_lm_generate."""
+    import ovnative_amd as ov
+    force = dict(band_wait=ov.FORCE_BAND_WAIT, xcd=ov.FORCE_XCD)[what]
+    ts, _ = make_lm(221, SMALL)
+    x = make_inputs(222, SMALL, 2, 300, 12)
+    ref = _lm(ts, SMALL)
+    ref.set_fused_norm(False)
+    want = ref.forward(*x)
+    lm = _lm(ts, SMALL)
+    try:
+        fused = lm.forward(*x)
+        assert lm.recovered() == 0
+        assert np.array_equal(fused.view(np.int32), want.view(np.int32))
+        lm.force_condition(force)
+        got = lm.forward(*x)
+        assert lm.recovered() == ov.RECOVERED_NORM
+        assert np.array_equal(got.view(np.int32), want.view(np.int32))
+        # the fallback is kept; the fused norm can be switched on again
+        assert np.array_equal(lm.forward(*x).view(np.int32), want.view(np.int32))
+        lm.set_fused_norm(True)
+        assert np.array_equal(lm.forward(*x).view(np.int32), want.view(np.int32))
+        assert lm.recovered() == ov.RECOVERED_NORM
+    finally:
+        lm.close()
+    Cb, V = SMALL["n_codebooks"], SMALL["audio_vocab"]
+    S, T = 300, 288
+    plane = S * Cb * V * 4
+    ref.set_device_sampling(True)
+    ref.forward(*x, host_logits=False)
+    base = ref.last_logits_ptr()
+    want_p, want_s = ref.sample(base, S, base + plane, S, T, 2.0, 5.0)
+    ref.set_device_sampling(False)
+    lm = _lm(ts, SMALL)
+    try:
+        lm.set_device_sampling(True)
+        lm.forward(*x, host_logits=False)       # fused, no flag: builds the layout's graph
+        lm.force_condition(force)
+        lm.forward(*x, host_logits=False)
+        base = lm.last_logits_ptr()
+        p, s = lm.sample(base, S, base + plane, S, T, 2.0, 5.0)
+        assert lm.recovered() == ov.RECOVERED_NORM
+        assert np.array_equal(p, want_p) and np.array_equal(s.view(np.int32), want_s.view(np.int32))
+    finally:
+        lm.close()
+    prompt = x[0][0].copy()
+    prompt[:, S - T:] = V - 1
+    opts = ov.GenOptions(num_steps=3)
+    want_t = ref.generate(prompt, x[1][0], T, opts)
+    lm = _lm(ts, SMALL)
+    try:
+        lm.force_condition(force)
+        got_t = lm.generate(prompt, x[1][0], T, opts)
+        assert lm.recovered() == ov.RECOVERED_NORM
+        assert np.array_equal(got_t, want_t)
+    finally:
+        lm.close()
+        ref.close()
+
+
+def test_stage_timer(small_lm):
+    """The stage timer (OV_CUDA_PROFILE's events, cuda_lm.cu:994-1022): one
+    time per stage, all positive, summing to about the forward; the logits are
+    the graph-replayed forward's bits."""
+    ts, table, lm = small_lm
+    x = make_inputs(231, SMALL, 2, 300, 12)
+    want = lm.forward(*x)
+    lm.set_profile(True)
+    try:
+        got = lm.forward(*x)
+        times = lm.stage_times()
+    finally:
+        lm.set_profile(False)
+    assert np.array_equal(got.view(np.int32), want.view(np.int32))
+    assert list(times) == ["prep+embed", "qkv", "attn", "o_proj", "gate_up", "down",
+                           "final_norm+head"], times
+    assert all(v > 0 for v in times.values()), times
+    print(f"stage times (ms, SMALL, B = 2, S = 300): {times}")
+    lm.forward(*x)  # graphs again
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 5 at its size: 8 requests x CFG 2 x seq 1024 (M = 16384, 16
+# attention segments), the 28-layer LM.
+
+def test_config5_forward_at_full_size(oracle, full_lm):
+    """The runner's forward of bench.py's config-5 batch (make_requests(8,
+    1024): each request a CFG pair, the uncond row masked as tts.cpp builds
+    it) at M = 16384: every request's logits equal, bit for bit, that request
+    run alone (M = 2048), and request 0 alone equals the oracle's forward
+    (lm.cpp:339-401) with the device attention substituted.  All three take
+    the same kernels: the large-M GEMM tiles (from 2048 rows), the norms as
+    launches of their own (fused only below 2048 rows; same bits either way)
+    and the long-sequence attention kernel (chosen by workgroup count: set
+    here for every size, since the short kernel sums in another order)."""
+    import bench
+    import ovnative_amd as ov
+    ts, table, lm = full_lm
+    ids, am, attn, pos = bench.make_requests(FULL28, 8, 1024)
+    B, Cb, S = ids.shape
+    assert (B, S) == (16, 1024)
+    prev = ov.set_attention_long_min_tasks(0)
+    try:
+        big = lm.forward(ids, am, attn, pos)              # [16, C, 1024, V]
+        for r in range(8):
+            sl = slice(2 * r, 2 * r + 2)
+            solo = lm.forward(ids[sl], am[sl], attn[sl], pos[sl])
+            assert np.array_equal(solo.view(np.int32), big[sl].view(np.int32)), r
+        V = big.shape[-1]
+        flat = big[:2].transpose(0, 2, 1, 3).reshape(2 * S, Cb * V)
+        del big
+        segs = [(attn[b], S, b * S) for b in range(2)]
+        hybrid = oracle.lm_forward(FULL28, table, ids[:2], am[:2], segs, pos[:2].reshape(-1),
+                                   attention=_device_attention(FULL28))
+        assert np.array_equal(flat.view(np.int32), hybrid.view(np.int32))
+    finally:
+        ov.set_attention_long_min_tasks(prev)
+
+
+def test_device_sampler_known_answer():
+    """The device sampler (ovh_lm_sample) on lm_fixture.SAMPLER_CASE, the
+    hand-worked case of tts.cpp:296-326 / cuda_lm.cu:679-758 (V = 4, two
+    codebooks): the hand-derived tokens and scores, and the flipped guidance
+    sign (g = -2) picks the other tokens."""
+    from lm_fixture import SAMPLER_CASE as K
+    cfg = dict(SMALL, n_layers=1, audio_vocab=K["V"], n_codebooks=K["C"])
+    ts, _ = make_lm(241, cfg)
+    lm = _lm(ts, cfg)
+    try:
+        cond = torch.tensor(K["cond"], dtype=torch.float32, device="cuda")
+        uncond = torch.tensor(K["uncond"], dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        pred, scores = lm.sample(cond.data_ptr(), 1, uncond.data_ptr(), 1, K["T"], K["guidance"],
+                                 K["penalty"])
+        assert np.array_equal(pred, np.array(K["pred"]))
+        np.testing.assert_allclose(scores, np.array(K["scores"]), rtol=0, atol=2e-6)
+        flipped, _ = lm.sample(cond.data_ptr(), 1, uncond.data_ptr(), 1, K["T"], -K["guidance"],
+                               K["penalty"])
+        assert np.array_equal(flipped, np.array([[1], [2]]))
+    finally:
+        lm.close()

@@ -242,6 +242,66 @@ def test_large_m_properties(oracle):
     assert np.array_equal(bits(C2), bits(C[perm]))
 
 
+def _sample_rows(rng, M, n):
+    """Rows of every large-M tile position: the first and last rows, the 64-row
+    tile edges around them, and random rows."""
+    edge = {0, 1, 31, 32, 63, 64, 127, 128, M // 2, M - 65, M - 64, M - 2, M - 1}
+    return np.array(sorted(edge | set(rng.choice(M, n, replace=False).tolist())))
+
+
+@pytest.mark.parametrize("which", ["silu_gate_up", "residual_k3072", "qkv_sliced_n4096"])
+def test_large_m_int8_form_sampled_rows(oracle, which):
+    """The default int8 GEMM form at M = 16384 (8 requests x
+    CFG 2 x seq 1024), i.e. the large-M tiles the runner takes from 2048 rows,
+    on the LM's shapes: the SiLU-fused gate/up (N = 2 x 3072, codes and scales
+    vs the oracle's sliced GEMM then silu_mul_quantize_f32), the down
+    projection's residual form (K = 3072, tile-major codes as the runner
+    passes them, accumulating into a random fp32 hidden state) and the merged
+    q/k/v sliced into three outputs (N = 2048 + 1024 + 1024); sampled rows
+    bit-exact vs the oracle."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng({"silu_gate_up": 71, "residual_k3072": 72,
+                                 "qkv_sliced_n4096": 73}[which])
+    M = 16384
+    if which == "silu_gate_up":
+        I, K = 3072, 1024
+        A = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+        qg, sg = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+        qu, su = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+        gu = ov.gate_up_weight(ov.Weight.from_host(qg, sg), ov.Weight.from_host(qu, su))
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        hq, hsc = ov.silu_gate_linear(aq, asc, gu)
+        hq, hsc = host(hq), host(hsc)
+        rows = _sample_rows(rng, M, 40)
+        hq_r, hsc_r = oracle.silu_mul_quantize(_oracle_linear(oracle, A[rows], qg, sg),
+                                               _oracle_linear(oracle, A[rows], qu, su))
+        assert np.array_equal(hq[rows], u8_to_s8(hq_r, I))
+        assert np.array_equal(bits(hsc[rows]), bits(hsc_r))
+    elif which == "residual_k3072":
+        N, K = 1024, 3072
+        A, Wf = _rand_problem(rng, M, N, K)
+        q, s = oracle.quantize_weight_rows(Wf)
+        w = ov.Weight.from_host(q, s)
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        Cin = rng.standard_normal((M, N)).astype(np.float32)
+        C = dev(Cin)
+        ov.linear_q_tiled(ov.tile_major(aq), asc, w, M, C, accumulate=True)
+        C = host(C)
+        rows = _sample_rows(rng, M, 40)
+        want = _oracle_linear(oracle, A[rows], q, s, Cin[rows])
+        assert np.array_equal(bits(C[rows]), bits(want))
+    else:
+        K = 1024
+        A, Wf = _rand_problem(rng, M, 4096, K)
+        q, s = oracle.quantize_weight_rows(Wf)
+        w = ov.Weight.from_host(q, s)
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        outs = ov.linear_q_sliced(aq, asc, w, [2048, 1024, 1024])
+        got = np.concatenate([host(o) for o in outs], axis=1)
+        rows = _sample_rows(rng, M, 40)
+        assert np.array_equal(bits(got[rows]), bits(_oracle_linear(oracle, A[rows], q, s)))
+
+
 # ---------------------------------------------------------------------------
 # the f16-operand GEMM form (opt-in, here from 2048 rows): int8-valued f16
 # weights and codes, exact block products out of the f16 matrix core.  Rows are
@@ -493,18 +553,22 @@ def test_linear_workspace_growth_and_streams(oracle, K):
 
 
 def test_linear_in_a_graph(oracle):
-    """ovh_linear captured once its stream's workspace fits: every replay
-    equals the eager result, with eager calls on that stream in between."""
+    """ovh_linear captured in a graph on a stream whose workspace would fit:
+    the captured call still quantises into a buffer the graph owns, so every
+    replay equals the eager result, also after eager calls on the capture
+    stream that grow (free and reallocate) that stream's workspace, and when
+    the graph is replayed on another stream."""
     import ovnative_amd as ov
     rng = np.random.default_rng(21)
     A, Wf = _rand_problem(rng, 200, 512, 1024)
     q, s = oracle.quantize_weight_rows(Wf)
     w = ov.Weight.from_host(q, s)
     want = bits(_oracle_linear(oracle, A, q, s))
-    s0 = torch.cuda.Stream()
+    s0, s1 = torch.cuda.Stream(), torch.cuda.Stream()
     dA, C = dev(A), torch.zeros((200, 512), dtype=torch.float32, device="cuda")
     A2, _ = _rand_problem(rng, 300, 1, 1024)
-    dA2 = dev(A2)
+    A3, _ = _rand_problem(rng, 1500, 1, 1024)
+    dA2, dA3 = dev(A2), dev(A3)
     with torch.cuda.stream(s0):
         ov.linear(dA2, w)                       # the workspace now holds 300 rows
     torch.cuda.synchronize()
@@ -512,15 +576,27 @@ def test_linear_in_a_graph(oracle):
     with torch.cuda.graph(g, stream=s0):
         ov.linear(dA, w, C)
     want2 = bits(_oracle_linear(oracle, A2, q, s))
-    for _ in range(3):
+    want3 = bits(_oracle_linear(oracle, A3, q, s))
+    for rep in range(3):
         C.fill_(7.0)
         g.replay()
         torch.cuda.synchronize()
-        assert np.array_equal(bits(host(C)), want)
+        assert np.array_equal(bits(host(C)), want), rep
+        with torch.cuda.stream(s0):
+            C3 = ov.linear(dA3, w)              # grows the workspace: frees the old buffer
+            C2 = ov.linear(dA2, w)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(host(C3)), want3), rep
+        assert np.array_equal(bits(host(C2)), want2), rep
+        C.fill_(7.0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s1):
+            g.replay()                          # the graph's buffer, not s1's or s0's
         with torch.cuda.stream(s0):
             C2 = ov.linear(dA2, w)
         torch.cuda.synchronize()
-        assert np.array_equal(bits(host(C2)), want2)
+        assert np.array_equal(bits(host(C)), want), rep
+        assert np.array_equal(bits(host(C2)), want2), rep
 
 
 def test_ldc_and_slices_errors(oracle):
@@ -743,7 +819,7 @@ def test_linear_q_norm_wait_running_out_is_flagged(oracle):
     t = ov.tile_major(aq)
     nw = dev(rng.uniform(0.5, 1.5, 1024).astype(np.float32))
     cnt = ov.band_counters()
-    stride = 32  # 64-bit words per counter slot: the error word's slot, then band 0's
+    stride = 64  # 64-bit words per counter slot: the error word's slot, then band 0's
     cnt[stride] = 1
     ov.linear_q_norm(t, asc, w, dev(np.zeros((32, 1024), np.float32)), nw, cnt)
     torch.cuda.synchronize()
@@ -757,6 +833,35 @@ def test_linear_q_norm_wait_running_out_is_flagged(oracle):
     assert host(cnt)[0] == 0
     assert np.array_equal(host(nq), tile_major(host(want_q), 32))
     assert np.array_equal(bits(host(nsc)), bits(host(want_s)))
+
+
+def test_linear_q_norm_counters_shared_across_widths(oracle):
+    """One counter buffer for launches of different widths and heights in any
+    order (each launch's band counters move on to the next launch boundary
+    whatever its column-tile count): every launch equals the two-call form and
+    the error word stays 0; the 64-row bands from 2048 rows share it too."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(9)
+    cnt = ov.band_counters(4096)
+    for M, N, K in [(600, 1024, 2048), (600, 256, 1024), (300, 512, 1024), (600, 1024, 3072),
+                    (37, 768, 1024), (2100, 1024, 1024), (600, 256, 1024), (2100, 512, 1024),
+                    (600, 1024, 2048)]:
+        A, Wf = _rand_problem(rng, M, N, K)
+        q, s = oracle.quantize_weight_rows(Wf)
+        w = ov.Weight.from_host(q, s)
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        t = ov.tile_major(aq)
+        nw = dev(rng.uniform(0.5, 1.5, N).astype(np.float32))
+        x0 = rng.standard_normal((M, N)).astype(np.float32)
+        x = dev(x0)
+        nq, nsc = ov.linear_q_norm(t, asc, w, x, nw, cnt)
+        want_x = dev(x0)
+        ov.linear_q_tiled(t, asc, w, M, want_x, accumulate=True)
+        want_q, want_s = ov.rmsnorm_quantize(want_x, nw, 1e-6)
+        assert host(cnt)[0] == 0, (M, N, K)
+        assert np.array_equal(bits(host(x)), bits(host(want_x))), (M, N, K)
+        assert np.array_equal(host(nq), tile_major(host(want_q), M)), (M, N, K)
+        assert np.array_equal(bits(host(nsc)), bits(host(want_s))), (M, N, K)
 
 
 def test_linear_q_norm_errors(oracle):

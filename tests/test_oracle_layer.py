@@ -286,3 +286,25 @@ def test_lm_forward_against_reference(reference, oracle, tmp_path, layout, batch
         cos = (got.astype(np.float64) * ref_flat).sum() / (
             np.linalg.norm(got.astype(np.float64)) * np.linalg.norm(ref_flat.astype(np.float64)))
         assert cos >= 0.9999
+
+
+def test_guided_sample_known_answer(oracle):
+    """The hand-worked case of lm_fixture.SAMPLER_CASE (derived there from
+    tts.cpp:296-326): the oracle's device-form sampler picks the hand-derived
+    tokens with the hand-derived scores (to fp32 rounding), and the case
+    separates the plausible mistakes: g = -2 computes the flipped guidance sign
+    (lc - 2 (lc - lu)) and picks tokens 1 and 2, g = 0 picks token 1 in
+    codebook 0, and the scores are far from the values without the second
+    log-softmax (1.9445, -7.0313)."""
+    from lm_fixture import SAMPLER_CASE as K
+    cond = np.array(K["cond"], np.float32)
+    uncond = np.array(K["uncond"], np.float32)
+
+    def run(g):
+        return oracle.guided_sample(cond, 1, uncond, K["C"], K["V"], K["T"], g, K["penalty"])
+    pred, scores = run(K["guidance"])
+    assert np.array_equal(pred, np.array(K["pred"]))
+    np.testing.assert_allclose(scores, np.array(K["scores"]), rtol=0, atol=2e-6)
+    assert np.array_equal(run(-K["guidance"])[0], np.array([[1], [2]]))
+    assert run(0.0)[0][0, 0] == 1
+    assert np.abs(scores - np.array([[1.9445], [-7.0313]])).min() > 0.05
