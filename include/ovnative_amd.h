@@ -249,6 +249,15 @@ int ovh_block_dots_tiled(int64_t M, const int8_t* aq, const OvhWeight* w, int32_
                          void* stream);
 int64_t ovh_tiled_codes_bytes(int64_t M, int64_t K);
 
+/* Diagnostics, no reference counterpart: read `bytes` of device memory at src
+ * once (bytes a positive multiple of 128 KiB) through one load path of the
+ * GEMM kernels: 0 DMA into LDS, 16 bytes a lane (the tiles of the 16x16
+ * kernels); 1 DMA into LDS, 4 bytes a lane; 2 16-byte vector loads; 3 8-byte
+ * buffer loads (the weight stream of the skinny grouped kernel).  Nothing is
+ * written.  For calibrating hardware byte counters (FETCH_SIZE) against a
+ * known byte count on exactly the paths the GEMMs use. */
+int ovh_diag_read(const void* src, int64_t bytes, int path, void* stream);
+
 /* ---- SiLU-gated MLP input ---------------------------------------------------
  * The reference composes gate/up -> silu*up -> quantise for the down
  * projection (cpp/src/model/lm.cpp:293-311: linear_s8_nk_packed_q_sliced over

@@ -55,6 +55,7 @@ SIGNATURES = {
     "ovh_weight_is_f32": (_int, [_p]),
     "ovh_linear_f32": (_int, [_i64, _p, _p, _p, _i64, _int, _p]),
     "ovh_block_dots": (_int, [_i64, _p, _p, _p, _p]),
+    "ovh_diag_read": (_int, [_p, _i64, _int, _p]),
     "ovh_block_dots_tiled": (_int, [_i64, _p, _p, _p, _p]),
     "ovh_tiled_codes_bytes": (_i64, [_i64, _i64]),
     "ovh_set_f16_min_rows": (_i64, [_i64]),
@@ -384,6 +385,11 @@ def linear_q_grouped(problems, outs=None, accumulate: bool = False):
         outs = [torch.empty((aq.shape[0], w.N), dtype=torch.float32, device="cuda")
                 for aq, _, w in problems]
     arr = (GemmGroup * max(1, len(problems)))()
+    for aq, asc, w in problems:
+        # the C ABI takes M from here and cannot see the buffers' sizes
+        if aq.dim() != 2 or aq.shape[1] < 32 * w.Kb or asc.shape[0] != aq.shape[0]:
+            raise InvalidArgument(OV_ERR_INVALID_ARG, "grouped GEMM: codes must be [M, Kp] row-major "
+                                  "with block scales [M, Kb]")
     for i, ((aq, asc, w), c) in enumerate(zip(problems, outs)):
         arr[i] = GemmGroup(aq.shape[0], _dptr(aq).value, _dptr(asc).value, w.handle.value,
                            _dptr(c).value, c.shape[1])
@@ -450,6 +456,16 @@ def block_dots(aq, w: Weight, M: int = None, tiled: bool = False):
     fn = load().ovh_block_dots_tiled if tiled else load().ovh_block_dots
     _check(fn(M, _dptr(aq), w.handle, _dptr(out), _stream()))
     return out
+
+
+READ_DMA16, READ_DMA4, READ_VEC16, READ_BUF8 = 0, 1, 2, 3
+
+
+def diag_read(t, path: int) -> None:
+    """Read tensor t's bytes once through one load path of the GEMM kernels
+    (READ_*), for calibrating hardware byte counters; t's size must be a
+    multiple of 128 KiB."""
+    _check(load().ovh_diag_read(_dptr(t), t.numel() * t.element_size(), path, _stream()))
 
 
 def gate_up_weight(gate: Weight, up: Weight) -> Weight:

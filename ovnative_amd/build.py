@@ -14,7 +14,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libovnative_amd.so")
-SOURCES = ["quant.hip", "gemm.hip", "gemm_f32.hip", "attn.hip", "capi.hip", "lm.hip"]
+SOURCES = ["quant.hip", "gemm.hip", "gemm_skinny.hip", "gemm_f32.hip", "attn.hip", "capi.hip",
+           "lm.hip", "diag.hip"]
 HOST_SOURCES = ["ovw1.cpp"]  # plain host C++ (no device code)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")

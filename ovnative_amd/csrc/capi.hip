@@ -735,6 +735,16 @@ int ovh_block_dots(int64_t M, const int8_t* aq, const OvhWeight* w, int32_t* out
   return block_dots(M, aq, w, out, stream, false);
 }
 
+int ovh_diag_read(const void* src, int64_t bytes, int path, void* stream) {
+  if (!src) return fail(OV_ERR_INVALID_ARG, "src is null");
+  if (path < 0 || path > 3) return fail(OV_ERR_INVALID_ARG, "path must be 0 .. 3");
+  if (bytes <= 0 || bytes % (128 * 1024) != 0 || bytes > (int64_t(128) << 30))
+    return fail(OV_ERR_INVALID_ARG, "bytes must be a positive multiple of 128 KiB (at most 128 GiB)");
+  OVH_HIP(ovh::launch_read_paths(static_cast<const int8_t*>(src), bytes, path, as_stream(stream)),
+          "diag read launch");
+  return OV_OK;
+}
+
 // ---- allocation-free linear -------------------------------------------------
 // ovh_linear quantises A into a stream-ordered allocation; this variant puts
 // the codes and scales in a fixed device array instead.  Each device holds its

@@ -190,6 +190,10 @@ struct GemmGroups {
   GemmArgs args[kMaxGroups];
 };
 hipError_t launch_gemm_grouped(const GemmGroups& gg, GemmMode mode, hipStream_t st);
+// The skinny-M form of a grouped launch (gemm_skinny.hip): every member with
+// M <= 128, K a multiple of 1024 up to 3072, int8 form, one output slice.
+bool skinny_applies(const GemmGroups& gg);
+hipError_t launch_gemm_skinny(const GemmGroups& gg, GemmMode mode, hipStream_t st);
 // Rows from which the GEMMs take the f16-operand form (GemmArgs::W16/aq16);
 // 0 (the default): never.  Measured on MI355X at M = 16384 the int8 form is the
 // faster one for the plain and residual GEMMs, so the f16 form is opt-in.
@@ -201,6 +205,10 @@ hipError_t launch_widen_f16(const int8_t* src, _Float16* dst, int64_t n, hipStre
 // row-major int8 codes [M][Kp] -> tile-major f16 codes (rows padded to 128).
 hipError_t launch_codes_to_f16_tiled(int64_t M, int64_t Kp, const int8_t* src, _Float16* dst,
                                      hipStream_t st);
+// Byte-counter calibration (diag.hip): read `bytes` (a multiple of 128 KiB)
+// from src once through one load path of the GEMM kernels.
+enum ReadPath { kReadDma16 = 0, kReadDma4 = 1, kReadVec16 = 2, kReadBuf8 = 3 };
+hipError_t launch_read_paths(const int8_t* src, int64_t bytes, int path, hipStream_t st);
 hipError_t launch_weight_layout(int64_t N, int64_t K, const int8_t* src, int layout,
                                 const float* scale_src, DeviceWeight& dst, hipStream_t st);
 hipError_t launch_weight_to_nk(const DeviceWeight& w, int8_t* q_nk, hipStream_t st);

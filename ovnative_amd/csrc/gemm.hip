@@ -1341,6 +1341,7 @@ hipError_t launch_gemm_grouped(const GemmGroups& in, GemmMode mode, hipStream_t 
   // 8-block stages, 21.1 for a 4-stage ring and 28-40 for 128-row tiles (whose
   // fewer workgroups each run a longer chain); from 2048 rows the large-M
   // tile, between the 32 x 32 tile of the mid-size band.
+  if (max_m <= 128 && skinny_applies(gg)) return launch_gemm_skinny(gg, mode, st);
   if (max_m < 256) return launch_grouped_cfg<32, 32, 2, 2, 4, 3, true>(gg, mode, st);
   if (max_m >= 2048) return launch_grouped_cfg<128, 64, 4, 2, 4, 2, false>(gg, mode, st);
   return launch_grouped_cfg<32, 32, 2, 2, 4, 2, true>(gg, mode, st);

@@ -202,6 +202,23 @@ def test_linear_vs_oracle(oracle, M, N, K):
     assert np.abs(C - R).max() / np.abs(R).max() < 5e-2  # quantisation noise bound, not parity
 
 
+def test_diag_read_paths():
+    """The byte-counter calibration reads run on every load path and leave the
+    buffer as it was; sizes that are not a multiple of 128 KiB and unknown paths
+    are refused."""
+    import ovnative_amd as ov
+    t = torch.arange(1 << 16, dtype=torch.float32, device="cuda")  # 256 KiB
+    ref = t.clone()
+    for path in (ov.READ_DMA16, ov.READ_DMA4, ov.READ_VEC16, ov.READ_BUF8):
+        ov.diag_read(t, path)
+    torch.cuda.synchronize()
+    assert torch.equal(t, ref)
+    with pytest.raises(ov.InvalidArgument):
+        ov.diag_read(t[:1000], ov.READ_DMA16)
+    with pytest.raises(ov.InvalidArgument):
+        ov.diag_read(t, 4)
+
+
 def test_block_dots_exact_at_scale(oracle):
     """Per-block int32 sums from the MFMA path equal integer brute force (sampled rows)."""
     import ovnative_amd as ov
@@ -445,6 +462,39 @@ def test_linear_q_grouped_equals_separate(oracle):
         want = dev(c)
         ov.linear_q(aq, asc, w, want, accumulate=True)
         assert np.array_equal(bits(host(g)), bits(host(want)))
+
+
+@pytest.mark.parametrize("accumulate", [False, True], ids=["store", "residual"])
+def test_linear_q_grouped_skinny(oracle, accumulate):
+    """The skinny-M form of the grouped launch (every member M <= 128 and K a
+    multiple of 1024 up to 3072: weights streamed into registers, activation
+    slab in LDS; 128 / 64 / 32 rows per workgroup for K = 1024 / 2048 / 3072):
+    ragged M (1 .. 128), widths that are not multiples of the 64-column
+    workgroup (96, 200, 1000), both output forms; every member equals its own
+    ovh_linear_q bit for bit and one the oracle."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(31 + accumulate)
+    cases = [(1, 1024, 1024), (17, 200, 2048), (64, 96, 3072), (100, 1000, 1024),
+             (128, 2048, 3072), (33, 1024, 2048), (128, 3072, 1024), (5, 512, 3072)]
+    probs, host_in = [], []
+    for M, n, k in cases:
+        A = rng.standard_normal((M, k)).astype(np.float32)
+        A[:, rng.choice(k, 8, replace=False)] *= 20
+        q, s = oracle.quantize_weight_rows((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        probs.append((aq, asc, ov.Weight.from_host(q, s)))
+        host_in.append((A, q, s))
+    cins = [rng.standard_normal((M, n)).astype(np.float32) for M, n, _ in cases]
+    got = [dev(c) for c in cins]
+    for i in range(0, len(probs), 4):  # two launches of four members
+        ov.linear_q_grouped(probs[i:i + 4], got[i:i + 4], accumulate=accumulate)
+    for (aq, asc, w), g, c in zip(probs, got, cins):
+        want = dev(c)
+        ov.linear_q(aq, asc, w, want, accumulate=accumulate)
+        assert np.array_equal(bits(host(g)), bits(host(want)))
+    A, q, s = host_in[4]
+    ref = _oracle_linear(oracle, A, q, s, cins[4] if accumulate else None)
+    assert np.array_equal(bits(host(got[4])), bits(ref))
 
 
 @pytest.mark.parametrize("Ms", [(600, 601, 37), (2100, 128, 5)], ids=["mid", "large"])
