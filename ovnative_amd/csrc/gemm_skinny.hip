@@ -67,7 +67,6 @@ template <int R, int KB>
 __device__ __forceinline__ void skinny_tile(const GemmArgs& a, int cb, int rg, int8_t* lds,
                                             bool accumulate) {
   constexpr int T = R / 32;   // 16-row MFMA tiles per wavefront (R / 2 rows)
-  constexpr int RT = R / 32;  // 32-row block tiles of the activation slab
   constexpr int KP = 32 * KB; // bytes of a row of codes
   static_assert(R * KP <= kSkActBytes && R * KB * 4 <= kSkSclBytes && KB % kRing == 0, "slab");
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
