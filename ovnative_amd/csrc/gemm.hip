@@ -1364,8 +1364,11 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
   // wavefronts (M = 128: 8.4 us against 11.4 for 128x64; M = 256: 9.8 against
   // 11.8 for 64x32 of two wavefronts); from M = 600 the 128x64 tile wins
   // with cache-hot weights (17.4 against 18.1 for the next).  At 512 < M < 1024
-  // (the LM step, whose weights come cold from HBM) the 256x64 tile of 8
-  // wavefronts: 16.0 against 17.4 us with cold weights.
+  // (the LM step, whose weights come cold from HBM) 8-wavefront tiles with the
+  // same 64x32 wavefront tile: 256x64 took 16.0 against 17.4 us for 128x64
+  // with cold weights, and 128x128 (half as many L2 re-reads of each weight
+  // tile, one per 128 rows) takes the step 2.256 against 2.265 ms for 256x64
+  // (four alternating pairs on one box).
   if (mode == kQkvNorm) return launch_qkv_norm(a, st);
   if (mode == kAccumNorm) return launch_gemm_norm(a, st);
   if ((a.W16 != nullptr) != (a.aq16 != nullptr)) return hipErrorInvalidValue;
@@ -1383,7 +1386,7 @@ hipError_t launch_gemm(const GemmArgs& a, GemmMode mode, hipStream_t st) {
     if (M >= 2048) return launch_cfg16_silu<128, 64, 2, 2, 4, 2, false>(a, st);
     if (M <= 128) return launch_cfg16_silu<128, 32, 2, 2, 4, 2, true>(a, st);
     if (M <= 512) return launch_cfg16_silu<64, 32, 1, 2, 4, 2, true>(a, st);
-    if (M < 1024 && a.N % 256 == 0) return launch_cfg16_silu<256, 64, 4, 2, 4, 2, true>(a, st);
+    if (M < 1024) return launch_cfg16_silu<128, 128, 2, 4, 4, 2, true>(a, st);
     return launch_cfg16_silu<128, 64, 2, 2, 4, 2, true>(a, st);
   }
   // kDumpBlocks takes the tile the store and residual modes take for the same
