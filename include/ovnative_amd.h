@@ -167,7 +167,10 @@ int ovh_linear_q_sliced(int64_t M, const int8_t* aq, const float* asc, const Ovh
  * lm.cpp:241-311); the results are those of ovh_linear_q bit for bit.  For
  * the skinny shapes (M < 256), where one launch per GEMM leaves most of the
  * GPU waiting on launch latency instead of streaming weights.  Every member's
- * K must be a multiple of 128 (OV_ERR_NOT_IMPLEMENTED otherwise). */
+ * K must be a multiple of 128 (OV_ERR_NOT_IMPLEMENTED otherwise).  When every
+ * member has M <= 128 and K of 1024, 2048 or 3072, with codes and scales
+ * 16-byte aligned, the launch stages each member's activation rows in LDS once
+ * and streams the weights straight into registers (same bits). */
 typedef struct OvhGemmGroup {
   int64_t M;
   const int8_t* aq;  /* row-major codes [M][Kp] */
