@@ -115,7 +115,10 @@ int ovh_silu_mul_quantize(int64_t M, int64_t K, const float* gate, const float* 
 /* ---- GEMM ------------------------------------------------------------------
  * C[m, n] = wscale[n] * sum_b fma-chain(float(acc_b[m,n]) * asc[m,b]) with
  * acc_b the exact int32 dot product of block b; bit-identical to the reference's
- * epilogue (gemm.cpp:469-502).  C has leading dimension ldc >= N.
+ * epilogue (gemm.cpp:469-502).  C has leading dimension ldc >= N.  The codes
+ * aq and the block scales asc are device pointers aligned to 16 bytes (the
+ * kernels move them by 16-byte DMA; OV_ERR_INVALID_ARG otherwise), as every
+ * allocation of the device allocator is.
  *
  * linear_s8_nk_packed_q (ov_gemm.h:98-100, gemm.cpp:758-774): accumulate = 0.
  * linear_s8_nk_packed_q_add (ov_gemm.h:78-80, gemm.cpp:847-862): accumulate = 1,

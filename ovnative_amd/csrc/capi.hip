@@ -73,6 +73,7 @@ int check_gemm_operands(int64_t M, const int8_t* aq, const float* asc, const Ovh
     return fail(OV_ERR_INVALID_ARG, "M and N must fit in 31 bits");
   if (!aq || !asc) return fail(OV_ERR_INVALID_ARG, "aq/asc must be device pointers");
   if (!aligned16(aq)) return fail(OV_ERR_INVALID_ARG, "aq must be 16-byte aligned");
+  if (!aligned16(asc)) return fail(OV_ERR_INVALID_ARG, "asc must be 16-byte aligned");
   return OV_OK;
 }
 

@@ -219,6 +219,29 @@ def test_diag_read_paths():
         ov.diag_read(t, 4)
 
 
+def test_linear_q_refuses_unaligned_scales():
+    """The GEMMs move codes and block scales by 16-byte DMA: scales that are
+    not 16-byte aligned are refused (single and grouped entry points) rather
+    than read from a rounded address; aligned copies of the same values give
+    the usual result."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(71)
+    M, N, K = 64, 256, 1024
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    w = ov.Weight.from_host(rng.integers(-127, 128, (N, K), dtype=np.int8),
+                            (rng.random(N) * 1e-3 + 1e-4).astype(np.float32))
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    flat = torch.empty(asc.numel() + 1, dtype=torch.float32, device="cuda")
+    mis = flat[1:].view(M, -1)  # 4 bytes past a 16-byte boundary
+    mis.copy_(asc)
+    with pytest.raises(ov.InvalidArgument):
+        ov.linear_q(aq, mis, w)
+    with pytest.raises(ov.InvalidArgument):
+        ov.linear_q_grouped([(aq, mis, w)])
+    assert np.array_equal(bits(host(ov.linear_q(aq, mis.clone(), w))),
+                          bits(host(ov.linear_q(aq, asc, w))))
+
+
 def test_block_dots_exact_at_scale(oracle):
     """Per-block int32 sums from the MFMA path equal integer brute force (sampled rows)."""
     import ovnative_amd as ov
