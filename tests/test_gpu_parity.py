@@ -202,6 +202,61 @@ def test_linear_vs_oracle(oracle, M, N, K):
     assert np.abs(C - R).max() / np.abs(R).max() < 5e-2  # quantisation noise bound, not parity
 
 
+BAND_EDGES = (127, 128, 129, 255, 256, 511, 512, 1023, 1024, 2047, 2048)
+
+
+@pytest.mark.parametrize("N,K", [(1024, 1024), (2048, 1024), (6144, 1024), (1024, 3072)])
+def test_linear_tile_band_edges(oracle, N, K):
+    """On both sides of every row count where launch_gemm changes tile shape
+    (128, 256, 512, 1024, 2048; with N = 1024 / 2048 / 6144 and K = 1024 /
+    3072, the N and K conditions of the dispatch): the store and residual
+    forms, on row-major and tile-major codes, are the oracle's bits
+    (gemm.cpp:432-504) on sampled rows, the first and last among them."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(N + K)
+    Mmax = max(BAND_EDGES)
+    A, Wf = _rand_problem(rng, Mmax, N, K)
+    q, s = oracle.quantize_weight_rows(Wf)
+    w = ov.Weight.from_host(q, s)
+    Cin = rng.standard_normal((Mmax, N)).astype(np.float32)
+    for M in BAND_EDGES:
+        aq, asc = ov.s8_nk_quantize(dev(A[:M]))
+        t = ov.tile_major(aq)
+        rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 6, replace=False)]))
+        want = _oracle_linear(oracle, A[rows], q, s)
+        want_acc = _oracle_linear(oracle, A[rows], q, s, Cin[rows])
+        for name, C in (("rowmajor", ov.linear_q(aq, asc, w)),
+                        ("tilemajor", ov.linear_q_tiled(t, asc, w, M))):
+            assert np.array_equal(bits(host(C)[rows]), bits(want)), (M, name)
+        for name, fn in (("rowmajor", lambda C: ov.linear_q(aq, asc, w, C, accumulate=True)),
+                         ("tilemajor",
+                          lambda C: ov.linear_q_tiled(t, asc, w, M, C, accumulate=True))):
+            C = dev(Cin[:M])
+            fn(C)
+            assert np.array_equal(bits(host(C)[rows]), bits(want_acc)), (M, name, "residual")
+
+
+@pytest.mark.parametrize("M", [129, 511, 512, 1023, 1024, 2047, 2048])
+def test_silu_gate_linear_band_edges(oracle, M):
+    """The SiLU-fused gate/up on both sides of its tile-shape changes (128,
+    512, 1024, 2048 rows): the reference's gate/up GEMM then
+    silu_mul_quantize_f32 (lm.cpp:293-311) byte for byte, on sampled rows."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(500 + M)
+    I, K = 3072, 1024
+    A = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    qg, sg = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    qu, su = oracle.quantize_weight_rows((rng.standard_normal((I, K)) * 0.02).astype(np.float32))
+    gu = ov.gate_up_weight(ov.Weight.from_host(qg, sg), ov.Weight.from_host(qu, su))
+    aq, asc = ov.s8_nk_quantize(dev(A))
+    hq, hsc = ov.silu_gate_linear(aq, asc, gu)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, 6, replace=False)]))
+    hq_r, hsc_r = oracle.silu_mul_quantize(_oracle_linear(oracle, A[rows], qg, sg),
+                                           _oracle_linear(oracle, A[rows], qu, su))
+    assert np.array_equal(host(hq)[rows], u8_to_s8(hq_r, I))
+    assert np.array_equal(bits(host(hsc)[rows]), bits(hsc_r))
+
+
 def test_diag_read_paths():
     """The byte-counter calibration reads run on every load path and leave the
     buffer as it was; sizes that are not a multiple of 128 KiB and unknown paths
@@ -844,7 +899,11 @@ def test_linear_q_tiled_equals_rowmajor(oracle, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(600, 1024, 2048), (600, 1024, 3072), (128, 1024, 3072),
                                    (1, 1024, 2048), (37, 256, 512), (300, 512, 1024),
                                    (1320, 1024, 2048), (2047, 768, 1024), (2048, 1024, 2048),
-                                   (4133, 1024, 3072), (2400, 256, 1024)])
+                                   (4133, 1024, 3072), (2400, 256, 1024),
+                                   # both sides of the tile-shape changes (256, 512, 1024 rows;
+                                   # K = 1024 with 8-block stages, 1152 without)
+                                   (255, 1024, 1024), (256, 1024, 1152), (511, 512, 3072),
+                                   (512, 1024, 1152), (1023, 1024, 2048), (1024, 256, 1024)])
 def test_linear_q_norm_equals_two_calls(oracle, M, N, K):
     """ovh_linear_q_norm (the runner's o_proj / down launch, with the RMSNorm +
     quantise that follows it: lm.cpp:281 + :292, :311 + :232) gives the bits of
