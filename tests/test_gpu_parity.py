@@ -575,11 +575,13 @@ def test_linear_q_grouped_skinny(oracle, accumulate):
     assert np.array_equal(bits(host(got[4])), bits(ref))
 
 
-@pytest.mark.parametrize("Ms", [(600, 601, 37), (2100, 128, 5)], ids=["mid", "large"])
+@pytest.mark.parametrize("Ms", [(600, 601, 37), (2100, 128, 5), (128, 128, 128), (129, 128, 1)],
+                         ids=["mid", "large", "skinny_edge", "past_skinny_edge"])
 def test_linear_q_grouped_tile_bands(oracle, Ms):
     """The grouped launch takes one tile shape for all members, chosen by the
-    largest M (32x32 tiles in the mid band, 128x64 tiles from 2048 rows): every
-    member, small ones included, still equals its own ovh_linear_q."""
+    largest M (the skinny kernel up to 128 rows, 32x32 tiles in the mid band,
+    128x64 tiles from 2048 rows): every member, small ones included, still
+    equals its own ovh_linear_q."""
     import ovnative_amd as ov
     rng = np.random.default_rng(sum(Ms))
     probs = []
