@@ -157,6 +157,40 @@ def test_attention_vs_oracle(oracle, seg_rows, nh, nkv, masked, split):
     assert np.all(got[dead] == 0)
 
 
+@pytest.mark.parametrize("seg_rows,nh,nkv,masked", [
+    ([300, 300], 16, 8, False),   # config 3/4 in the long form
+    ([300, 260], 16, 8, True),
+    ([640, 3], 8, 2, True),       # a segment shorter than the 128-row tile: dead wavefronts
+    ([1, 33, 64, 65], 4, 2, True),
+    ([700], 4, 4, False),         # KV group of 1
+    ([7], 2, 2, False),
+])
+def test_attention_long_form_forced(oracle, seg_rows, nh, nkv, masked):
+    """The long-sequence split form (K/V blocks through LDS, every wavefront
+    walking all keys; chosen by workgroup count, here forced for every size
+    with ovh_set_attention_long_min_tasks(0)) on short and ragged segments,
+    where some of its wavefronts have no query rows and only move K/V: within
+    the attention tolerance of the oracle (ops_cpu.cpp:907-943), fully masked
+    rows exactly zero, and the threshold restored afterwards."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(7 * sum(seg_rows) + nh)
+    D = 128
+    segs, T = _segments(rng, seg_rows, masked)
+    q = rng.standard_normal((T, nh * D)).astype(np.float32)
+    k = rng.standard_normal((T, nkv * D)).astype(np.float32)
+    v = rng.standard_normal((T, nkv * D)).astype(np.float32)
+    want = oracle.attention(q, k, v, segs, nh, nkv, D)
+    dsegs = [(None if b is None else dev(b), rows, r0, k0) for b, rows, r0, k0 in segs]
+    prev = ov.set_attention_long_min_tasks(0)
+    try:
+        got = host(ov.attention(dev(q), dev(k), dev(v), dsegs, nh, nkv, D, split=True))
+    finally:
+        assert ov.set_attention_long_min_tasks(prev) == 0
+    assert _attn_err(got, want) <= ATTN_TOL
+    dead = np.all(want == 0, axis=1)
+    assert np.all(got[dead] == 0)
+
+
 def test_attention_sharp_and_argument_errors(oracle):
     """Large logits (softmax close to one-hot) and the ABI's argument checks."""
     import ovnative_amd as ov
