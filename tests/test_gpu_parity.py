@@ -236,6 +236,45 @@ def test_linear_tile_band_edges(oracle, N, K):
             assert np.array_equal(bits(host(C)[rows]), bits(want_acc)), (M, name, "residual")
 
 
+def test_linear_random_shapes(oracle):
+    """Seeded random shapes (M up to 2600; N and K ragged, or multiples of 128
+    / 256 as the LM's are): ovh_linear_q is the oracle's bits on sampled rows,
+    and where the shape allows them ovh_linear_q_tiled and ovh_linear_q_norm
+    (== the residual launch then ovh_rmsnorm_quantize) are too."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(2026)
+    for _ in range(24):
+        M = int(rng.choice([rng.integers(1, 300), rng.integers(300, 2600)]))
+        N = int(rng.choice([rng.integers(1, 700), 256 * rng.integers(1, 5), 2048, 3072]))
+        K = int(rng.choice([rng.integers(1, 600), 128 * rng.integers(1, 25), 1024, 3072]))
+        A, Wf = _rand_problem(rng, M, N, K, outliers=min(8, K))
+        q, s = oracle.quantize_weight_rows(Wf)
+        w = ov.Weight.from_host(q, s)
+        aq, asc = ov.s8_nk_quantize(dev(A))
+        rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, min(M, 5), replace=False)]))
+        want = _oracle_linear(oracle, A[rows], q, s)
+        assert np.array_equal(bits(host(ov.linear_q(aq, asc, w))[rows]), bits(want)), (M, N, K)
+        if K % 128:
+            continue
+        t = ov.tile_major(aq)
+        got = host(ov.linear_q_tiled(t, asc, w, M))[rows]
+        assert np.array_equal(bits(got), bits(want)), (M, N, K, "tiled")
+        if N % 256 or N > 1024:
+            continue
+        x0 = rng.standard_normal((M, N)).astype(np.float32)
+        nw = dev(rng.uniform(0.5, 1.5, N).astype(np.float32))
+        cnt = ov.band_counters(max(M, 2048))
+        x = dev(x0)
+        nq, nsc = ov.linear_q_norm(t, asc, w, x, nw, cnt, 1e-6)
+        want_x = dev(x0)
+        ov.linear_q_tiled(t, asc, w, M, want_x, accumulate=True)
+        want_q, want_s = ov.rmsnorm_quantize(want_x, nw, 1e-6)
+        assert np.array_equal(bits(host(x)), bits(host(want_x))), (M, N, K, "norm")
+        assert np.array_equal(host(nq), tile_major(host(want_q), M)), (M, N, K, "norm codes")
+        assert np.array_equal(bits(host(nsc)), bits(host(want_s))), (M, N, K, "norm scales")
+        assert host(cnt)[0] == 0
+
+
 @pytest.mark.parametrize("M", [129, 511, 512, 1023, 1024, 2047, 2048])
 def test_silu_gate_linear_band_edges(oracle, M):
     """The SiLU-fused gate/up on both sides of its tile-shape changes (128,
