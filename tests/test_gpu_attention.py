@@ -191,6 +191,35 @@ def test_attention_long_form_forced(oracle, seg_rows, nh, nkv, masked):
     assert np.all(got[dead] == 0)
 
 
+def test_attention_random_segments(oracle):
+    """Seeded random segment layouts (1 to 4 segments of 1 to 700 rows, KV
+    groups of 1, 2 and 4, with and without masks), each through the fp32 form,
+    the split form as chosen by size, and the split form's long kernel forced:
+    within the attention tolerance of the oracle, fully masked rows zero."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(4242)
+    D = 128
+    for _ in range(8):
+        nh, nkv = [(16, 8), (8, 2), (4, 4), (2, 1)][rng.integers(4)]
+        rows = [int(r) for r in rng.integers(1, 701, rng.integers(1, 5))]
+        segs, T = _segments(rng, rows, bool(rng.integers(2)))
+        q = rng.standard_normal((T, nh * D)).astype(np.float32)
+        k = rng.standard_normal((T, nkv * D)).astype(np.float32)
+        v = rng.standard_normal((T, nkv * D)).astype(np.float32)
+        want = oracle.attention(q, k, v, segs, nh, nkv, D)
+        dead = np.all(want == 0, axis=1)
+        dsegs = [(None if b is None else dev(b), r, r0, k0) for b, r, r0, k0 in segs]
+        for split, long_min in ((False, None), (True, None), (True, 0)):
+            prev = ov.set_attention_long_min_tasks(long_min) if long_min is not None else None
+            try:
+                got = host(ov.attention(dev(q), dev(k), dev(v), dsegs, nh, nkv, D, split=split))
+            finally:
+                if prev is not None:
+                    ov.set_attention_long_min_tasks(prev)
+            assert _attn_err(got, want) <= ATTN_TOL, (rows, nh, nkv, split, long_min)
+            assert np.all(got[dead] == 0), (rows, nh, nkv, split, long_min)
+
+
 def test_attention_sharp_and_argument_errors(oracle):
     """Large logits (softmax close to one-hot) and the ABI's argument checks."""
     import ovnative_amd as ov
