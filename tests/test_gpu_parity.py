@@ -634,6 +634,35 @@ def test_linear_q_grouped_tile_bands(oracle, Ms):
         assert np.array_equal(bits(host(c)), bits(host(ov.linear_q(aq, asc, w))))
 
 
+def test_linear_q_grouped_random(oracle):
+    """Seeded random groups of 1 to 8 members (M 1 .. 200, so that some groups
+    take the skinny kernel and some the 16x16 tiles; N ragged or the LM's; K a
+    multiple of 128, mostly the LM's 1024 / 2048 / 3072), store and residual
+    forms: every member equals its own ovh_linear_q bit for bit."""
+    import ovnative_amd as ov
+    rng = np.random.default_rng(808)
+    for it in range(10):
+        n_mem = int(rng.integers(1, 9))
+        probs, cins = [], []
+        for _ in range(n_mem):
+            M = int(rng.integers(1, 201 if it % 2 else 129))
+            N = int(rng.choice([rng.integers(1, 700), 1024, 2048, 3072]))
+            K = int(rng.choice([1024, 2048, 3072, 128 * rng.integers(1, 12)]))
+            A = rng.standard_normal((M, K)).astype(np.float32)
+            q, s = oracle.quantize_weight_rows((rng.standard_normal((N, K)) * 0.02)
+                                               .astype(np.float32))
+            aq, asc = ov.s8_nk_quantize(dev(A))
+            probs.append((aq, asc, ov.Weight.from_host(q, s)))
+            cins.append(rng.standard_normal((M, N)).astype(np.float32))
+        accumulate = bool(it % 3 == 0)
+        got = [dev(c) for c in cins]
+        ov.linear_q_grouped(probs, got, accumulate=accumulate)
+        for j, ((aq, asc, w), g, c) in enumerate(zip(probs, got, cins)):
+            want = dev(c)
+            ov.linear_q(aq, asc, w, want, accumulate=accumulate)
+            assert np.array_equal(bits(host(g)), bits(host(want))), (it, j)
+
+
 def test_linear_q_grouped_errors(oracle):
     import ovnative_amd as ov
     rng = np.random.default_rng(3)
