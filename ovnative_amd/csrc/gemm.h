@@ -26,14 +26,14 @@ enum GemmMode {
 // band's counter once its stores are in that XCD's L2, and the last
 // GemmArgs::n_helpers to arrive (the launcher picks up to kMaxNormHelpers)
 // wait for the count to complete and normalise the band's rows.  The
-// counters are 64-bit, one 512-byte slot (kBandCntStride words) per band,
-// zero when allocated.  A launch's arrivals at a band start at a multiple of
-// kBandRound, and the band's last arrival moves the counter on to the next
-// multiple, so a counter buffer serves launches of any column-tile count in
-// any order.  Words 1 .. 32 of a slot are the tags of the band's column
-// tiles: each workgroup writes (launch boundary << 4 | its XCC_ID) there
-// before it counts itself, and the helpers check, once the count is
-// complete, that every tile's tag is this launch's and names their own XCD.
+// counters are 64-bit words, kBandCntStride words apart, zero when allocated:
+// bits 0-15 count the band's arrivals, bits 16 + 6x .. 21 + 6x those that
+// ran on XCD x, each workgroup adding to both in one atomic.  A launch's
+// arrivals start at a multiple of kBandRound in the arrival field (0 or
+// 2^15), and the band's last arrival moves the word on to the other one with
+// the XCD fields cleared, so a counter buffer serves launches of any
+// column-tile count in any order.  That last arrival also checks that all
+// of the band's tiles counted on its own XCD.
 // Error bits of GemmArgs::norm_err: kNormErrWait, a band's wait ran out or
 // its counter was not at a launch boundary; kNormErrXcd, a tile of the band
 // ran on another XCD than its helpers (its rows may then have been
@@ -42,7 +42,11 @@ enum GemmMode {
 constexpr int kMaxNormHelpers = 16;
 constexpr int kBandCntStride = 64;
 constexpr int kMaxBandTiles = 32;
-constexpr unsigned long long kBandRound = 1ull << 16;
+constexpr unsigned long long kBandRound = 1ull << 15;
+constexpr unsigned long long kBandCountMask = 0xFFFFull;
+constexpr int kBandXccShift = 16, kBandXccBits = 6;
+static_assert(kMaxBandTiles < (1 << kBandXccBits) && kBandXccShift + 8 * kBandXccBits <= 64,
+              "eight XCD fields of the band counter");
 constexpr uint32_t kNormErrWait = 2u, kNormErrXcd = 4u;
 // XCDs the band placement assumes (workgroup id % 8 -> one XCD per residue:
 // the dispatcher hands workgroups to the XCDs round-robin, from an XCD that

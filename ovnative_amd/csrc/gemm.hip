@@ -976,30 +976,25 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     unsigned long long* const cnt = a.band_cnt + (int64_t)mtile * kBandCntStride;
     unsigned long long* const bc = reinterpret_cast<unsigned long long*>(&smem[0][0]);
     const unsigned long long nt = (unsigned long long)n_tiles;  // <= kMaxBandTiles (host)
-    // XCC_ID: hardware register 20, bits 0-3
-    const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11));
-    // the tile's tag (bit 4: written in this launch; the XCD it ran on), in L2
-    // with the tile's result before the count
-    if (threadIdx.x == 0)
-      __hip_atomic_store(cnt + 1 + ntile,
-                         16ull | (unsigned long long)(xcc ^ ((a.xcd_test && (ntile & 1)) ? 1 : 0)),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // XCC_ID: hardware register 20, bits 0-3 (0 .. 7 on the devices the launcher
+    // accepts)
+    const int xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 7;
+    // The count: 1 in the arrival field and 1 in the field of the XCD the tile
+    // ran on (another one for the odd tiles when the host forces a mismatch),
+    // in one atomic, so the band's last arrival can tell whether every tile
+    // ran on its XCD.
+    const int xc = xcc ^ ((a.xcd_test && (ntile & 1)) ? 1 : 0);
+    const unsigned long long mine = 1ull + (1ull << (kBandXccShift + kBandXccBits * xc));
     wait_vm_lgkm<0>();
     __syncthreads();  // every wavefront's stores drained; the ring is free
-    if (threadIdx.x == 0) {
-      const unsigned long long v0 =
-          __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // the band's last arrival moves the counter on to the next launch
-      // boundary (nothing of this launch arrives after it)
-      if (v0 % kBandRound == nt - 1)
-        __hip_atomic_fetch_add(cnt, kBandRound - nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bc[0] = v0;
-    }
+    if (threadIdx.x == 0)
+      bc[0] = __hip_atomic_fetch_add(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const unsigned long long v = bc[0];
+    const unsigned long long low = v & kBandCountMask;
     const unsigned long long helpers =
         nt < (unsigned long long)a.n_helpers ? nt : (unsigned long long)a.n_helpers;
-    const unsigned long long arrived = v % kBandRound;  // this launch's arrivals before this one
+    const unsigned long long arrived = low % kBandRound;  // this launch's arrivals before this one
     if (arrived >= nt) {
       // the counter was not at a launch boundary when this launch began
       if (threadIdx.x == 0)
@@ -1008,15 +1003,16 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     }
     if (arrived < nt - helpers) return;
     // Wait for the band's last arrival: agent-scope loads read the counter in
-    // L2.  At most n_helpers - 1 workgroups of a band wait, and only once
-    // their own tile is done; the launcher keeps their number over the
+    // L2, until its arrival field is nt past this launch's boundary (modulo
+    // the field).  At most n_helpers - 1 workgroups of a band wait, and only
+    // once their own tile is done; the launcher keeps their number over the
     // XCD's bands below its workgroup slots, so the bands' other workgroups
     // can always run.  The wait is bounded all the same; one that runs out
     // sets kNormErrWait.
     if (threadIdx.x == 0) {
-      const unsigned long long target = v - arrived + nt;
-      for (int it = 0; (long long)(__hip_atomic_load(cnt, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT) - target) < 0;
+      const unsigned long long base = low - arrived;
+      for (int it = 0; ((__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - base) &
+                        kBandCountMask) < nt;
            ++it) {
         if (it == (1 << 18)) {
           __hip_atomic_fetch_or(a.norm_err, kNormErrWait, __ATOMIC_RELAXED,
@@ -1032,17 +1028,6 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
     // L1 may hold lines of them from before the other workgroups' stores (an
     // L1 invalidate would do too, but buffer_inv sc1 also drops the XCD's
     // clean L2 lines, which the band's neighbours are still reading).
-    // The band's last arrival checks the tags (their loads issued here, the
-    // comparison after its rows, so the check adds no wait): every other tile
-    // counted itself before it, each after its tag was in L2, so every tag of
-    // this launch is in this XCD's L2 and names this XCD.  A tile that ran on
-    // another XCD left its tag, like its rows, in that XCD's L2 (here the
-    // consumed tag of the last launch is read), or names that XCD.  Then the
-    // tags are consumed.
-    const bool checker = arrived == nt - 1 && threadIdx.x < nt;
-    unsigned long long tag = 0;
-    if (checker) tag = __hip_atomic_load(cnt + 1 + threadIdx.x, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
     const int h = (int)(arrived - (nt - helpers));
     float* const xt = reinterpret_cast<float*>(&smem[0][0]) + wave * kRmsRowLds<4>;
     for (int rr = h + (int)helpers * wave; rr < BM; rr += (int)helpers * NW) {
@@ -1065,10 +1050,25 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
           break;
       }
     }
-    if (checker) {
-      if (tag != (16ull | (unsigned long long)xcc))
+    if (arrived == nt - 1 && threadIdx.x == 0) {
+      // The band's last arrival: the word as every arrival of this launch left
+      // it; every tile ran on this XCD iff all nt count in its field (a tile
+      // on another XCD counted there, and its rows stayed in that XCD's L2).
+      // Then the word moves to the other launch boundary with the XCD fields
+      // cleared, by a store (no arrival of this launch is left to add to it;
+      // the waiting helpers' condition holds for both values, 2^15 past their
+      // boundary; the next launch on this counter starts after this one has
+      // ended), here at the end rather than beside the count, where the
+      // workgroup's barrier would wait for it.  Measured: an agent-scope
+      // atomic add there instead cost ~0.2 us per launch, beside the count
+      // ~0.6 us.
+      const unsigned long long fin = v + mine;
+      const unsigned long long here = (fin >> (kBandXccShift + kBandXccBits * xcc)) &
+                                      ((1ull << kBandXccBits) - 1);
+      if (here != nt)
         __hip_atomic_fetch_or(a.norm_err, kNormErrXcd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(cnt + 1 + threadIdx.x, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long next = ((fin & kBandCountMask) - nt) ^ kBandRound;
+      __hip_atomic_store(cnt, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
 }

@@ -1064,6 +1064,10 @@ def test_linear_q_norm_counters_shared_across_widths(oracle):
         assert np.array_equal(bits(host(x)), bits(host(want_x))), (M, N, K)
         assert np.array_equal(host(nq), tile_major(host(want_q), M)), (M, N, K)
         assert np.array_equal(bits(host(nsc)), bits(host(want_s))), (M, N, K)
+        # between launches every band word stands at a launch boundary (0 or
+        # 2^15 arrivals) with its per-XCD arrival fields cleared
+        words = host(cnt).view(np.uint64)[64::64]
+        assert np.all((words & np.uint64(0x7FFF)) == 0) and np.all((words >> np.uint64(16)) == 0)
 
 
 def test_linear_q_norm_errors(oracle):
