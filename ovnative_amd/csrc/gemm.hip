@@ -968,9 +968,9 @@ __device__ __forceinline__ void gemm16_tile(const GemmArgs& a, const int wg) {
 
   if constexpr (MODE == kAccumNorm) {
     // The band hand-off.  Once vmcnt has drained, this workgroup's result
-    // stores are in the XCD's L2, where the band's counter add is performed
-    // after them (atomics execute in L2; the counter's 512-byte slot is this
-    // band's alone, so no other XCD holds it).
+    // stores are in the XCD's L2, and the band's counter add follows them
+    // (the counter's 512-byte slot is this band's alone: within a launch only
+    // the band's XCD touches it).
     static_assert(BM % 32 == 0, "bands of whole 32-row block tiles");
     static_assert(NW * kRmsRowLds<4> * 4 + 16 <= NST * STAGE, "the row norm's LDS fits in the ring");
     unsigned long long* const cnt = a.band_cnt + (int64_t)mtile * kBandCntStride;
