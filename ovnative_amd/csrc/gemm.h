@@ -141,9 +141,10 @@ struct GemmArgs {
   unsigned long long* band_cnt = nullptr;
   uint32_t* norm_err = nullptr;
   int n_helpers = 8;  // set by the launcher
-  // kAccumNorm test support: non-zero makes the odd column tiles' tags name
-  // another XCD, so the helpers' placement check fails (the condition forced
-  // from the host; every workgroup still ends normally).  0 in use.
+  // kAccumNorm test support: non-zero makes the odd column tiles count in
+  // another XCD's arrival field, so the band's placement check fails (the
+  // condition forced from the host; every workgroup still ends normally).  0
+  // in use.
   int xcd_test = 0;
 };
 
